@@ -1,0 +1,116 @@
+/*
+ * C ABI of the MI355X (gfx950) causal grouped-query attention library
+ * (libmt_attn.so).  Plain pointers and sizes only; no torch types.
+ *
+ * These entry points replace the reference's operator boundary for its
+ * attention hot path (paths relative to the duoan/mega-trading tree):
+ *
+ *   mt_gqa_attn_fwd  <- _TritonCausalAttention.forward,
+ *                       src/mega_trading/kernels/triton_attention.py:28-78
+ *                       (the kernel launches at :40-74).  With rope_cos /
+ *                       rope_sin set it also replaces the RoPE launch that
+ *                       precedes it, triton_apply_rope / _TritonRoPE.forward,
+ *                       src/mega_trading/kernels/triton_ops.py:45-54,187-202,
+ *                       as called from src/mega_trading/model.py:223.
+ *   mt_gqa_attn_bwd  <- _TritonCausalAttention.backward,
+ *                       src/mega_trading/kernels/triton_attention.py:80-111,
+ *                       and _triton_attention_server_backward :134-245
+ *                       (dQ kernel :154, dK/dV kernel :197).  With RoPE tables
+ *                       it also replaces _TritonRoPE.backward,
+ *                       src/mega_trading/kernels/triton_ops.py:204-214.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are device pointers on the current HIP device.
+ *   - Tensors are [B, H, T, D]; strides are in elements and ordered
+ *     (b, h, t, d); the d stride must be 1 (the others are free, so the
+ *     [B, T, H, D]-physical views the model produces are accepted as is).
+ *   - K and V have Hkv heads, Q / O / dO / dQ have Hq = Hkv * repeats heads;
+ *     query head h reads KV head h / repeats (triton_attention.py:299).
+ *   - Causal, top-left aligned, Tq == Tk == T, any T >= 1.
+ *   - D in {32, 64, 128}; dtype MT_DTYPE_BF16 or MT_DTYPE_FP16.
+ *   - lse and delta_ws are fp32 [B, Hq, T] contiguous; lse is the natural-log
+ *     logsumexp of the scaled scores (triton_attention.py:346-349).
+ *   - rope_cos / rope_sin: either both NULL (no RoPE) or both fp32
+ *     [>= T, D/2] contiguous tables, row t = position t
+ *     (src/mega_trading/model.py:279-284).  The rotation acts on interleaved
+ *     pairs (x[2i], x[2i+1]) (model.py:312-316).
+ *   - stream is a hipStream_t (NULL = the legacy default stream).  Calls are
+ *     asynchronous, never synchronise, never allocate device memory, and are
+ *     safe to record into a HIP graph.
+ *   - Return 0 on success.  Negative values are argument errors
+ *     (MT_E_*), positive values are hipError_t codes from the launch.
+ *     mt_last_error() describes the most recent failure of the calling thread.
+ */
+#ifndef MT_ATTENTION_H_
+#define MT_ATTENTION_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MT_DTYPE_BF16 0
+#define MT_DTYPE_FP16 1
+
+#define MT_OK 0
+#define MT_E_NULL (-1)     /* a required pointer is NULL */
+#define MT_E_SHAPE (-2)    /* B/H/T/D/repeats inconsistent or unsupported */
+#define MT_E_STRIDE (-3)   /* d stride != 1, or misaligned rows */
+#define MT_E_DTYPE (-4)    /* dtype code not supported */
+#define MT_E_ROPE (-5)     /* exactly one of rope_cos / rope_sin given */
+
+/* Library version, (major << 16) | minor. */
+int mt_version(void);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char* mt_last_error(void);
+
+/*
+ * Forward.  O = softmax(scale * rot(Q) rot(K)^T + causal) V and its LSE.
+ *   q [B,Hq,T,D], k/v [B,Hkv,T,D], o [B,Hq,T,D] (written), lse [B,Hq,T] (written).
+ *   strides: 16 int64 = q, k, v, o, 4 each in (b, h, t, d) order.
+ */
+int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                    int B, int Hq, int Hkv, int T, int D,
+                    const int64_t* strides, float scale, int dtype,
+                    const float* rope_cos, const float* rope_sin, void* stream);
+
+/*
+ * Backward.  Given dO, writes dQ, dK, dV (in the un-rotated basis when RoPE
+ * tables are given) and uses delta_ws [B,Hq,T] fp32 as scratch
+ * (delta = rowsum(O * dO), triton_attention.py:561).
+ *   strides: 32 int64 = q, k, v, o, dO, dQ, dK, dV, 4 each in (b, h, t, d) order.
+ *   dQ/dK/dV are fully overwritten (no zero-fill needed).
+ */
+int mt_gqa_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                    const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
+                    int B, int Hq, int Hkv, int T, int D,
+                    const int64_t* strides, float scale, int dtype,
+                    const float* rope_cos, const float* rope_sin, void* stream);
+
+/*
+ * The two halves of mt_gqa_attn_bwd, for callers that schedule or time the
+ * backward kernels separately (same arguments and conventions).
+ *   mt_gqa_attn_bwd_dq  <- _triton_attention_backward_dq_server_kernel launch,
+ *                          triton_attention.py:154-195; writes dQ and delta_ws.
+ *   mt_gqa_attn_bwd_dkv <- _triton_attention_backward_dkv_server_kernel launch,
+ *                          triton_attention.py:197-244; reads delta_ws, so it
+ *                          must follow mt_gqa_attn_bwd_dq on the same stream.
+ */
+int mt_gqa_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                       const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
+                       int B, int Hq, int Hkv, int T, int D,
+                       const int64_t* strides, float scale, int dtype,
+                       const float* rope_cos, const float* rope_sin, void* stream);
+int mt_gqa_attn_bwd_dkv(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
+                        int B, int Hq, int Hkv, int T, int D,
+                        const int64_t* strides, float scale, int dtype,
+                        const float* rope_cos, const float* rope_sin, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MT_ATTENTION_H_ */

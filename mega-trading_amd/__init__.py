@@ -1,0 +1,17 @@
+"""MI355X-native causal grouped-query attention for the mega-trading decoder.
+
+Import with ``importlib.import_module("mega-trading_amd")`` (the directory
+name carries a hyphen).  Public API:
+
+* ``attention(query, key, value, *, repeats)`` -- drop-in for the reference's
+  ``triton_attention`` (``src/mega_trading/kernels/triton_attention.py:12``).
+* ``rope_attention(query, key, value, cos, sin, *, repeats)`` -- the same with
+  the interleaved RoPE of ``model.py:223`` fused into the kernels.
+* ``attention_forward(...)`` -- forward returning ``(output, logsumexp)``.
+* ``model`` -- the Llama-style order-flow decoder that calls them
+  (``attention_backend="hip"``).
+"""
+
+from .attention import SUPPORTED_HEAD_DIMS, attention, attention_forward, rope_attention
+
+__all__ = ["attention", "rope_attention", "attention_forward", "SUPPORTED_HEAD_DIMS"]

@@ -1,0 +1,252 @@
+"""Causal grouped-query attention on MI355X (gfx950) HIP kernels.
+
+Drop-in for the reference operator
+``mega_trading.kernels.triton_attention.triton_attention(query, key, value, *, repeats)``
+(``src/mega_trading/kernels/triton_attention.py:12-24``): same argument
+meaning, same validation order and exception types, output with the query's
+layout, LSE saved for the backward.  ``rope_attention`` additionally fuses the
+interleaved RoPE that ``model.py:223`` applies right before the attention call
+(``triton_apply_rope``, ``src/mega_trading/kernels/triton_ops.py:45-54``) into
+the kernels' Q/K tile loads.
+
+Both ops are ``torch.library`` custom ops (``mega_trading_amd::gqa_attn_fwd``
+and ``::gqa_attn_bwd``) with fake implementations, so ``torch.compile`` treats
+them as opaque nodes.  They launch on the caller's current stream, never
+synchronise and never fall back to another implementation: without the HIP
+library they raise.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _native
+
+__all__ = ["attention", "rope_attention", "attention_forward", "SUPPORTED_HEAD_DIMS"]
+
+SUPPORTED_HEAD_DIMS = (32, 64, 128)
+_KERNEL_DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16}
+
+
+def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, repeats: int) -> torch.Tensor:
+    """Causal GQA attention (``triton_attention.py:12``).
+
+    ``query`` [B, Hq, T, D]; ``key``/``value`` [B, Hkv, T, D] with
+    ``Hq == Hkv * repeats``; query head ``h`` attends to KV head ``h // repeats``.
+    Scale ``1/sqrt(D)``, top-left causal mask.  Any strides with a unit last
+    stride are used in place.  fp32 inputs run through the bf16 kernels and
+    come back as fp32 (the reference's fp32 path likewise computes its dots at
+    reduced precision, TF32).
+    """
+    _validate(query, key, value, repeats)
+    out, _lse = _forward(query, key, value, None, None)
+    return out
+
+
+def rope_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    *,
+    repeats: int,
+) -> torch.Tensor:
+    """RoPE(query), RoPE(key), then causal GQA attention, in one fused op.
+
+    Equivalent to ``model.py:223`` + ``:226``: ``query, key = rope(query, key)``
+    then ``triton_attention(query, key, value, repeats=repeats)``, with the
+    rotation done in fp32 inside the kernels' tile loads.  ``cos``/``sin`` are
+    the RotaryEmbedding tables (``model.py:279-284``): fp32, last dim D/2,
+    leading singleton dims allowed, at least T rows; row t rotates position t.
+    Gradients w.r.t. query and key are returned in the un-rotated basis.
+    """
+    _validate(query, key, value, repeats)
+    c, s = _rope_tables(cos, sin, query)
+    out, _lse = _forward(query, key, value, c, s)
+    return out
+
+
+def attention_forward(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    repeats: int,
+    cos: Optional[torch.Tensor] = None,
+    sin: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward returning ``(output, logsumexp)``; LSE is fp32 [B, Hq, T], natural log
+    (``triton_attention.py:346-349``).  Differentiable in the output."""
+    _validate(query, key, value, repeats)
+    c = s = None
+    if cos is not None or sin is not None:
+        if cos is None or sin is None:
+            raise ValueError("cos and sin must be given together")
+        c, s = _rope_tables(cos, sin, query)
+    return _forward(query, key, value, c, s)
+
+
+# ---------------------------------------------------------------------------
+# validation (triton_attention.py:14-23) and argument preparation
+# ---------------------------------------------------------------------------
+def _validate(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, repeats: int) -> None:
+    if query.device.type != "cuda":
+        raise RuntimeError("hip attention backend requires ROCm GPU tensors")
+    if query.dtype not in {torch.float16, torch.bfloat16, torch.float32}:
+        raise RuntimeError("hip attention supports float16, bfloat16, and float32 tensors")
+    if query.ndim != 4 or key.ndim != 4 or value.ndim != 4:
+        raise ValueError("query, key, and value must be [batch, heads, sequence, head_dim]")
+    if key.shape[1] * repeats != query.shape[1]:
+        raise ValueError("query heads must equal key/value heads multiplied by repeats")
+    if key.shape != value.shape:
+        raise ValueError("key and value must have the same shape")
+    if query.shape[0] != key.shape[0] or query.shape[2:] != key.shape[2:]:
+        raise ValueError("query, key, and value must agree on batch, sequence, and head dimensions")
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise RuntimeError("query, key, and value must share one dtype")
+    if key.device != query.device or value.device != query.device:
+        raise RuntimeError("query, key, and value must be on one device")
+    if query.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS} (got {query.shape[-1]})")
+    if query.shape[2] < 1 or query.shape[0] < 1:
+        raise ValueError("batch and sequence length must be positive")
+
+
+def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    t, d = query.shape[2], query.shape[3]
+    out = []
+    for name, tab in (("cos", cos), ("sin", sin)):
+        if tab.shape[-1] != d // 2:
+            raise ValueError(f"RoPE {name} table must have last dimension head_dim/2 = {d // 2}")
+        tab2 = tab.reshape(-1, d // 2)
+        if tab2.shape[0] < t:
+            raise ValueError(f"sequence length {t} exceeds RoPE cache length {tab2.shape[0]}")
+        out.append(tab2[:t].to(device=query.device, dtype=torch.float32).contiguous())
+    return out[0], out[1]
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """Unit last stride, 8-element-aligned outer strides and a 16-byte-aligned base."""
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+    if ok:
+        for size, stride in zip(t.shape[:-1], t.stride()[:-1]):
+            if size > 1 and stride % 8:
+                ok = False
+                break
+    return t if ok else t.contiguous()
+
+
+def _strides(*tensors: torch.Tensor):
+    flat = []
+    for t in tensors:
+        flat.extend(int(st) if sz > 1 else 0 for sz, st in zip(t.shape, t.stride()))
+    import ctypes
+
+    return (ctypes.c_int64 * len(flat))(*flat)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _forward(q, k, v, cos, sin):
+    if q.dtype == torch.float32:
+        o, lse = _forward(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), cos, sin)
+        return o.to(torch.float32), lse
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    return torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, v, cos, sin, scale)
+
+
+# ---------------------------------------------------------------------------
+# custom ops
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("mega_trading_amd::gqa_attn_fwd", mutates_args=(), device_types="cuda")
+def gqa_attn_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: Optional[torch.Tensor],
+    sin: Optional[torch.Tensor],
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _native.load()
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    b, hq, t, d = q.shape
+    hkv = k.shape[1]
+    out = torch.empty_like(q)
+    out = _kernel_ready(out)
+    lse = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
+    strides = _strides(q, k, v, out)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.mt_gqa_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
+        )
+    _native.check(rc, "mt_gqa_attn_fwd")
+    return out, lse
+
+
+@gqa_attn_fwd.register_fake
+def _gqa_attn_fwd_fake(q, k, v, cos, sin, scale):
+    return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
+
+
+@torch.library.custom_op("mega_trading_amd::gqa_attn_bwd", mutates_args=(), device_types="cuda")
+def gqa_attn_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    dout: torch.Tensor,
+    cos: Optional[torch.Tensor],
+    sin: Optional[torch.Tensor],
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    lib = _native.load()
+    q, k, v, o = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(o)
+    dout = _kernel_ready(dout.to(q.dtype))
+    lse = lse.contiguous()
+    b, hq, t, d = q.shape
+    hkv = k.shape[1]
+    dq = _kernel_ready(torch.empty_like(q))
+    dk = _kernel_ready(torch.empty_like(k))
+    dv = _kernel_ready(torch.empty_like(v))
+    delta = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
+    strides = _strides(q, k, v, o, dout, dq, dk, dv)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.mt_gqa_attn_bwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dout.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+            b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
+        )
+    _native.check(rc, "mt_gqa_attn_bwd")
+    return dq, dk, dv
+
+
+@gqa_attn_bwd.register_fake
+def _gqa_attn_bwd_fake(q, k, v, o, lse, dout, cos, sin, scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _fwd_setup_context(ctx, inputs, output):
+    q, k, v, cos, sin, scale = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, out, lse, cos, sin)
+    ctx.scale = scale
+    ctx.mark_non_differentiable(lse)
+
+
+def _fwd_backward(ctx, grad_out, _grad_lse):
+    q, k, v, out, lse, cos, sin = ctx.saved_tensors
+    dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q, k, v, out, lse, grad_out, cos, sin, ctx.scale)
+    return dq, dk, dv, None, None, None
+
+
+gqa_attn_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)

@@ -1,0 +1,99 @@
+// Shared device helpers for the gfx950 causal GQA attention kernels.
+//
+// MFMA layout facts used throughout (v_mfma_f32_32x32x16_{bf16,f16}, wave64),
+// checked lane by lane on an MI355X:
+//   A operand (32 x 16, M x K): lane l holds row m = l % 32, k-slots 8*(l/32) + j, j = 0..7
+//   B operand (16 x 32, K x N): lane l holds col n = l % 32, k-slots 8*(l/32) + j
+//   C/D (32 x 32):              lane l holds col n = l % 32, rows m = 8*(i/4) + 4*(l/32) + (i%4), i = 0..15
+// A k-slot (half h, slot j) of A pairs with the same (h, j) of B, so any
+// permutation of the contraction index that is applied to both operands gives
+// the same product.  The kernels exploit that: a C tile (lane = n, slots = m)
+// is fed straight back as the B operand of a product that contracts over m,
+// with the A operand read in the matching permuted order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mt {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element traits: storage is always 16-bit; the MFMA builtin differs.
+struct BF16 {
+  using v8 = bf16x8;
+  using v4 = bf16x4;
+  using v2 = bf16x2;
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+};
+
+struct FP16 {
+  using v8 = f16x8;
+  using v4 = f16x4;
+  using v2 = f16x2;
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f(uint16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+};
+
+// Two fp32 values -> two 16-bit values packed in a u32 (round to nearest even).
+template <class E>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  f32x2 x = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, typename E::v2));
+}
+
+// Low/high 16-bit halves of a u32 as fp32.
+template <class E>
+__device__ __forceinline__ float lo_f(uint32_t w) { return E::to_f(uint16_t(w & 0xffffu)); }
+template <class E>
+__device__ __forceinline__ float hi_f(uint32_t w) { return E::to_f(uint16_t(w >> 16)); }
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Max of a value and its lane^32 partner (both halves of the wave end up equal).
+__device__ __forceinline__ float max_with_partner(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_with_partner(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Rotate the 4 interleaved pairs held in a 16-byte chunk (8 x 16-bit) by the
+// angles whose cos/sin are c[0..3], s[0..3]:  (e, o) -> (e c - o s, e s + o c).
+template <class E>
+__device__ __forceinline__ u32x4 rope_chunk(u32x4 x, f32x4 c, f32x4 s) {
+  u32x4 out;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    float e = lo_f<E>(x[p]);
+    float o = hi_f<E>(x[p]);
+    out[p] = pack2<E>(e * c[p] - o * s[p], e * s[p] + o * c[p]);
+  }
+  return out;
+}
+
+__device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
+
+}  // namespace mt

@@ -1,0 +1,141 @@
+"""CPU tests of the drop-in boundary: the C ABI library and the Python operator.
+
+No compute call is made here.  The C ABI checks run on arguments that fail
+validation before any launch; the Python checks run under FakeTensorMode,
+which yields "cuda" tensors without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mt_attention.h")
+
+
+def _header_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mt_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol(mta):
+    lib = mta._native.load()
+    declared = _header_functions()
+    assert declared == sorted(mta._native.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/mt_attention.h but not exported"
+    assert lib.mt_version() == (0 << 16) | 1
+
+
+def test_library_is_gfx950_only(mta):
+    data = open(mta._native.library_path(), "rb").read()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100", b"sm_"):
+        assert b"amdgcn-amd-amdhsa--" + other not in data
+
+
+def _fwd_call(lib, q=0x1000, k=0x1000, v=0x1000, o=0x1000, lse=0x1000, b=1, hq=4, hkv=2, t=16, d=64,
+              strides=None, dtype=0, cos=None, sin=None):
+    if strides is None:
+        strides = [hq * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hq * t * d, t * d, d, 1]
+    arr = (ctypes.c_int64 * 16)(*strides)
+    return lib.mt_gqa_attn_fwd(q, k, v, o, lse, b, hq, hkv, t, d, arr, 0.125, dtype, cos, sin, None)
+
+
+def test_c_abi_rejects_bad_arguments_before_launch(mta):
+    lib = mta._native.load()
+    E_NULL, E_SHAPE, E_STRIDE, E_DTYPE, E_ROPE = -1, -2, -3, -4, -5
+    assert _fwd_call(lib, q=None) == E_NULL
+    assert b"q is NULL" in lib.mt_last_error()
+    assert _fwd_call(lib, lse=None) == E_NULL
+    assert _fwd_call(lib, hq=5, hkv=2) == E_SHAPE
+    assert b"repeats" in lib.mt_last_error()
+    assert _fwd_call(lib, d=48) == E_SHAPE
+    assert _fwd_call(lib, t=0) == E_SHAPE
+    assert _fwd_call(lib, dtype=7) == E_DTYPE
+    assert _fwd_call(lib, cos=0x1000, sin=None) == E_ROPE
+    assert _fwd_call(lib, cos=0x1008, sin=0x1008) == E_ROPE  # misaligned tables
+    bad = [4 * 16 * 64, 16 * 64, 64, 2] + [2 * 16 * 64, 16 * 64, 64, 1] * 2 + [4 * 16 * 64, 16 * 64, 64, 1]
+    assert _fwd_call(lib, strides=bad) == E_STRIDE
+    assert b"last-dim stride" in lib.mt_last_error()
+    odd = [4 * 16 * 64, 16 * 64, 65, 1] + [2 * 16 * 64, 16 * 64, 64, 1] * 2 + [4 * 16 * 64, 16 * 64, 64, 1]
+    assert _fwd_call(lib, strides=odd) == E_STRIDE
+    assert _fwd_call(lib, q=0x1002) == E_STRIDE  # misaligned base
+    arr = (ctypes.c_int64 * 32)(*([1] * 32))
+    assert lib.mt_gqa_attn_bwd(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, None,
+                               1, 4, 2, 16, 64, arr, 0.125, 0, None, None, None) == E_NULL
+    assert b"delta_ws" in lib.mt_last_error()
+    for name in ("mt_gqa_attn_bwd_dq", "mt_gqa_attn_bwd_dkv"):
+        fn = getattr(lib, name)
+        assert fn(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000,
+                  1, 4, 2, 16, 33, arr, 0.125, 0, None, None, None) == E_SHAPE
+
+
+def test_error_codes_raise_python_errors(mta):
+    with pytest.raises(mta._native.HipAttentionError, match="head_dim"):
+        mta._native.check(_fwd_call(mta._native.load(), d=40), "mt_gqa_attn_fwd")
+
+
+# ---------------------------------------------------------------------------
+# Python operator validation: same checks, order and types as
+# src/mega_trading/kernels/triton_attention.py:14-23
+# ---------------------------------------------------------------------------
+def test_cpu_tensors_are_rejected_like_the_reference(mta):
+    q = torch.randn(1, 4, 8, 32)
+    k = torch.randn(1, 2, 8, 32)
+    with pytest.raises(RuntimeError, match="requires ROCm GPU tensors"):
+        mta.attention(q, k, k, repeats=2)
+
+
+def _fake(shape, dtype=torch.bfloat16):
+    return torch.empty(shape, device="cuda", dtype=dtype)
+
+
+def test_validation_errors_on_device_tensors(mta):
+    with FakeTensorMode():
+        q, k = _fake((1, 4, 8, 64)), _fake((1, 2, 8, 64))
+        with pytest.raises(RuntimeError, match="float16, bfloat16, and float32"):
+            mta.attention(_fake((1, 4, 8, 64), torch.int32), k, k, repeats=2)
+        with pytest.raises(ValueError, match="multiplied by repeats"):
+            mta.attention(q, k, k, repeats=4)
+        with pytest.raises(ValueError, match="same shape"):
+            mta.attention(q, k, _fake((1, 2, 9, 64)), repeats=2)
+        with pytest.raises(ValueError, match="agree on batch"):
+            mta.attention(q, _fake((1, 2, 9, 64)), _fake((1, 2, 9, 64)), repeats=2)
+        with pytest.raises(ValueError, match="head_dim"):
+            mta.attention(_fake((1, 4, 8, 48)), _fake((1, 2, 8, 48)), _fake((1, 2, 8, 48)), repeats=2)
+        with pytest.raises(RuntimeError, match="share one dtype"):
+            mta.attention(q, _fake((1, 2, 8, 64), torch.float16), k, repeats=2)
+        cos = torch.empty(4, 32, device="cuda")
+        with pytest.raises(ValueError, match="exceeds RoPE cache length"):
+            mta.rope_attention(q, k, k, cos, cos, repeats=2)
+        with pytest.raises(ValueError, match="head_dim/2"):
+            mta.rope_attention(q, k, k, torch.empty(8, 31, device="cuda"), torch.empty(8, 31, device="cuda"), repeats=2)
+
+
+def test_fake_impls_give_shapes_for_tracing(mta):
+    with FakeTensorMode():
+        q, k = _fake((2, 8, 100, 64)), _fake((2, 2, 100, 64))
+        out, lse = torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, k, None, None, 0.125)
+        assert out.shape == q.shape and lse.shape == (2, 8, 100) and lse.dtype == torch.float32
+        dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q, k, k, out, lse, q, None, None, 0.125)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+
+
+def test_kernel_ready_keeps_model_layout_views():
+    """The [B,T,H,D]-physical views of model.py:220-222 pass through without a copy."""
+    import importlib
+
+    ops = importlib.import_module("mega-trading_amd.attention")
+    x = torch.randn(2, 16, 8, 64).transpose(1, 2)  # [B, H, T, D] view
+    assert ops._kernel_ready(x) is x
+    y = torch.randn(2, 8, 16, 64)[..., ::2]  # non-unit last stride -> copy
+    assert ops._kernel_ready(y).is_contiguous()
+    arr = ops._strides(torch.empty(1, 1, 5, 32))
+    assert list(arr) == [0, 0, 32, 1]  # size-1 dims pass stride 0
