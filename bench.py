@@ -1,0 +1,265 @@
+"""Benchmark: causal GQA fwd+bwd on one MI355X, the reference's headline metric.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+* step: one forward + backward of the fused-RoPE causal GQA op over one batch
+  of BASELINE config 3 (B=4, T=4096, Hq=16, Hkv=4, D=64, bf16, RoPE theta 1e4,
+  Q/K/V ~ N(0, 0.5^2), dO ~ N(0, 1)), inputs resident in HBM.
+* value: TFLOP/s with the reference's FLOP convention extended to fwd+bwd,
+  14 * B * Hq * D * T(T+1)/2 (scripts/benchmark_triton_attention.py:179-190
+  gives the forward 4 * B * Hq * D * T(T+1)/2; backward adds 2.5x).
+* roofline: the dominant kernel's algorithmic MFMA FLOPs per launch over its
+  average duration, timed live with HIP events on the launch stream.
+* cpu_baseline: the reference's CPU attention path (torch SDPA, fp32, forward
+  + autograd backward, model.py:228-235) on the host cores over a bounded
+  sample of the same workload.
+* secondary: BASELINE config 2 (T=1024) fwd+bwd TFLOP/s and the un-fused op.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
+METRIC = "causal GQA fwd+bwd TFLOP/s (% bf16 MFMA peak) at T=1k/4k; train tokens/sec"
+
+# (B, T, Hq, Hkv, D)
+C2 = (16, 1024, 8, 2, 64)
+C3 = (4, 4096, 16, 4, 64)
+
+# algorithmic MFMA FLOPs per launch, in units of B * Hq * D * T(T+1)/2
+KERNEL_FLOP_UNITS = {
+    "attn_fwd_kernel": 4,      # S = QK^T, O = PV
+    "attn_bwd_dq_kernel": 6,   # S, dP recomputed; dQ = dS K
+    "attn_bwd_dkv_kernel": 8,  # S, dP recomputed; dV = P^T dO, dK = dS^T Q
+}
+
+
+def pairs(t: int) -> int:
+    return t * (t + 1) // 2
+
+
+def fwd_bwd_flops(b, t, hq, d) -> float:
+    return 14.0 * b * hq * d * pairs(t)
+
+
+def make_inputs(cfg, device, seed=0):
+    b, t, hq, hkv, d = cfg
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(b, hq, t, d, generator=g) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(b, hkv, t, d, generator=g) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(b, hkv, t, d, generator=g) * 0.5).to(torch.bfloat16)
+    do = torch.randn(b, hq, t, d, generator=g).to(torch.bfloat16)
+    return [x.to(device) for x in (q, k, v, do)]
+
+
+def rope_tables(t, d, theta, device):
+    """RotaryEmbedding buffers as model.py:279-284 builds them (fp32)."""
+    pos = torch.arange(t, dtype=torch.float32)
+    inv_freq = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    freqs = torch.outer(pos, inv_freq)
+    return freqs.cos().to(device), freqs.sin().to(device)
+
+
+def time_op_steps(pkg, cfg, steps, warmup, rope=True):
+    """Wall time of `steps` fwd+bwd steps through the public op (events + sync)."""
+    b, t, hq, hkv, d = cfg
+    dev = torch.device("cuda:0")
+    q, k, v, do = make_inputs(cfg, dev)
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    cos, sin = rope_tables(t, d, 10_000.0, dev)
+
+    def step():
+        if rope:
+            out = pkg.rope_attention(q, k, v, cos, sin, repeats=hq // hkv)
+        else:
+            out = pkg.attention(q, k, v, repeats=hq // hkv)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall / steps * 1e3
+
+
+def time_kernels(pkg, cfg, iters):
+    """Average duration of each kernel, HIP events recorded on its launch stream."""
+    native = pkg._native
+    lib = native.load()
+    b, t, hq, hkv, d = cfg
+    dev = torch.device("cuda:0")
+    q, k, v, do = make_inputs(cfg, dev)
+    cos, sin = rope_tables(t, d, 10_000.0, dev)
+    o = torch.empty_like(q)
+    lse = torch.empty((b, hq, t), device=dev, dtype=torch.float32)
+    q_rot, k_rot = torch.empty_like(q), torch.empty_like(k)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws_bytes = lib.mt_gqa_attn_bwd_workspace_size(b, hq, hkv, t, d)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    s_fwd = native.strides_array(q, k, v, o)
+    s_bwd = native.strides_array(q_rot, k_rot, v, o, do, dq, dk, dv)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    scale = 1.0 / math.sqrt(d)
+
+    def fwd():
+        native.check(lib.mt_gqa_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                         q_rot.data_ptr(), k_rot.data_ptr(),
+                                         b, hq, hkv, t, d, s_fwd, scale, 0, cos.data_ptr(), sin.data_ptr(), sp), "fwd")
+
+    def bwd(fn):
+        native.check(fn(q_rot.data_ptr(), k_rot.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(),
+                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
+                        b, hq, hkv, t, d, s_bwd, scale, 0, cos.data_ptr(), sin.data_ptr(), sp), "bwd")
+
+    stages = [("attn_fwd_kernel", fwd), ("attn_bwd_dq_kernel", lambda: bwd(lib.mt_gqa_attn_bwd_dq)),
+              ("attn_bwd_dkv_kernel", lambda: bwd(lib.mt_gqa_attn_bwd_dkv))]
+    for _ in range(3):
+        for _, fn in stages:
+            fn()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(iters)]
+    for i in range(iters):
+        ev[i][0].record(stream)
+        for j, (_, fn) in enumerate(stages):
+            fn()
+            ev[i][j + 1].record(stream)
+    torch.cuda.synchronize()
+    out = {}
+    for j, (name, _) in enumerate(stages):
+        ms = sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(iters)) / iters
+        flops = KERNEL_FLOP_UNITS[name] * b * hq * d * pairs(t)
+        out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flop": flops}
+    return out
+
+
+def cpu_baseline(cfg):
+    """Reference CPU attention (torch SDPA fp32 fwd + autograd bwd) on one batch
+    element of the workload, 1 warm-up + 3 timed repeats, median."""
+    from oracle.sdpa_cpu import sdpa_forward_backward
+
+    b, t, hq, hkv, d = cfg
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    sample = (1, t, hq, hkv, d)
+    q, k, v, do = (x.float() for x in make_inputs(sample, "cpu"))
+    times = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        sdpa_forward_backward(q, k, v, do, repeats=hq // hkv)
+        if rep:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": fwd_bwd_flops(1, t, hq, d) / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": f"torch SDPA fp32 fwd+bwd (reference eager path, model.py:228-235) on 1 of {b} batch elements "
+                  f"of the workload (B=1,T={t},Hq={hq},Hkv={hkv},D={d}), median of 3 after 1 warm-up: "
+                  f"{med * 1e3:.1f} ms; host '{model}', os.cpu_count()={os.cpu_count()}",
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the path is single-GPU; got --gpus {args.gpus})", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        return 2
+    pkg = importlib.import_module("mega-trading_amd")
+    pkg._native.load()
+
+    b, t, hq, hkv, d = C3
+    ms_event, ms_wall = time_op_steps(pkg, C3, args.steps, args.warmup, rope=True)
+    flops = fwd_bwd_flops(b, t, hq, d)
+    value = flops / (ms_event * 1e-3) / 1e12
+
+    kern = time_kernels(pkg, C3, max(10, args.steps // 2))
+    dom = max(kern, key=lambda n: kern[n]["ms"])
+    achieved = kern[dom]["tflops"]
+
+    ms_c2, _ = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)
+    ms_c3_plain, _ = time_op_steps(pkg, C3, max(10, args.steps // 2), 3, rope=False)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_event, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 3: causal GQA fwd+bwd, fused RoPE (theta 1e4), B=4 T=4096 Hq=16 Hkv=4 D=64 bf16",
+            "B": b, "T": t, "Hq": hq, "Hkv": hkv, "D": d,
+        },
+        "pct_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dom,
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1)} for n, x in kern.items()},
+        "secondary": {
+            "C2_fwd_bwd_tflops": round(fwd_bwd_flops(*C2[:1], C2[1], C2[2], C2[4]) / (ms_c2 * 1e-3) / 1e12, 2),
+            "C2_ms_per_step": round(ms_c2, 4),
+            "C3_unfused_rope_free_tflops": round(flops / (ms_c3_plain * 1e-3) / 1e12, 2),
+            "wall_ms_per_step": round(ms_wall, 4),
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(C3)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

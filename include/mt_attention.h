@@ -28,8 +28,8 @@
  *     query head h reads KV head h / repeats (triton_attention.py:299).
  *   - Causal, top-left aligned, Tq == Tk == T, any T >= 1.
  *   - D in {32, 64, 128}; dtype MT_DTYPE_BF16 or MT_DTYPE_FP16.
- *   - lse and delta_ws are fp32 [B, Hq, T] contiguous; lse is the natural-log
- *     logsumexp of the scaled scores (triton_attention.py:346-349).
+ *   - lse is fp32 [B, Hq, T] contiguous, the natural-log logsumexp of the
+ *     scaled scores (triton_attention.py:346-349).
  *   - rope_cos / rope_sin: either both NULL (no RoPE) or both fp32
  *     [>= T, D/2] contiguous tables, row t = position t
  *     (src/mega_trading/model.py:279-284).  The rotation acts on interleaved
@@ -44,6 +44,7 @@
 #ifndef MT_ATTENTION_H_
 #define MT_ATTENTION_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -54,11 +55,12 @@ extern "C" {
 #define MT_DTYPE_FP16 1
 
 #define MT_OK 0
-#define MT_E_NULL (-1)     /* a required pointer is NULL */
-#define MT_E_SHAPE (-2)    /* B/H/T/D/repeats inconsistent or unsupported */
-#define MT_E_STRIDE (-3)   /* d stride != 1, or misaligned rows */
-#define MT_E_DTYPE (-4)    /* dtype code not supported */
-#define MT_E_ROPE (-5)     /* exactly one of rope_cos / rope_sin given */
+#define MT_E_NULL (-1)      /* a required pointer is NULL */
+#define MT_E_SHAPE (-2)     /* B/H/T/D/repeats inconsistent or unsupported */
+#define MT_E_STRIDE (-3)    /* d stride != 1, or misaligned rows / buffers */
+#define MT_E_DTYPE (-4)     /* dtype code not supported */
+#define MT_E_ROPE (-5)      /* exactly one of rope_cos / rope_sin given */
+#define MT_E_WORKSPACE (-6) /* backward workspace smaller than required */
 
 /* Library version, (major << 16) | minor. */
 int mt_version(void);
@@ -70,21 +72,33 @@ const char* mt_last_error(void);
  * Forward.  O = softmax(scale * rot(Q) rot(K)^T + causal) V and its LSE.
  *   q [B,Hq,T,D], k/v [B,Hkv,T,D], o [B,Hq,T,D] (written), lse [B,Hq,T] (written).
  *   strides: 16 int64 = q, k, v, o, 4 each in (b, h, t, d) order.
+ *   With RoPE tables: q_rot [B,Hq,T,D] and k_rot [B,Hkv,T,D] (contiguous,
+ *   written) receive the rotated Q and K; the backward consumes them in place
+ *   of q and k.  Without tables both may be NULL.
  */
 int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                    void* q_rot, void* k_rot,
                     int B, int Hq, int Hkv, int T, int D,
                     const int64_t* strides, float scale, int dtype,
                     const float* rope_cos, const float* rope_sin, void* stream);
 
+/* Bytes of device workspace mt_gqa_attn_bwd needs for this shape on the
+ * current device (0 for an invalid shape). */
+size_t mt_gqa_attn_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D);
+
 /*
- * Backward.  Given dO, writes dQ, dK, dV (in the un-rotated basis when RoPE
- * tables are given) and uses delta_ws [B,Hq,T] fp32 as scratch
- * (delta = rowsum(O * dO), triton_attention.py:561).
+ * Backward.  Given dO, writes dQ, dK, dV.
+ *   q, k: the tensors the forward's scores were computed from -- q_rot and
+ *   k_rot when RoPE tables are given, in which case dQ and dK are rotated back
+ *   by -theta and returned in the un-rotated basis (triton_ops.py:205-214).
+ *   workspace: 256-byte aligned device buffer of at least
+ *   mt_gqa_attn_bwd_workspace_size() bytes (delta = rowsum(O * dO),
+ *   triton_attention.py:561, and fp32 dK/dV partial sums).
  *   strides: 32 int64 = q, k, v, o, dO, dQ, dK, dV, 4 each in (b, h, t, d) order.
  *   dQ/dK/dV are fully overwritten (no zero-fill needed).
  */
 int mt_gqa_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
-                    const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
+                    const void* dout, void* dq, void* dk, void* dv, void* workspace, size_t workspace_size,
                     int B, int Hq, int Hkv, int T, int D,
                     const int64_t* strides, float scale, int dtype,
                     const float* rope_cos, const float* rope_sin, void* stream);
@@ -93,18 +107,18 @@ int mt_gqa_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
  * The two halves of mt_gqa_attn_bwd, for callers that schedule or time the
  * backward kernels separately (same arguments and conventions).
  *   mt_gqa_attn_bwd_dq  <- _triton_attention_backward_dq_server_kernel launch,
- *                          triton_attention.py:154-195; writes dQ and delta_ws.
+ *                          triton_attention.py:154-195; writes dQ and delta.
  *   mt_gqa_attn_bwd_dkv <- _triton_attention_backward_dkv_server_kernel launch,
- *                          triton_attention.py:197-244; reads delta_ws, so it
+ *                          triton_attention.py:197-244; reads delta, so it
  *                          must follow mt_gqa_attn_bwd_dq on the same stream.
  */
 int mt_gqa_attn_bwd_dq(const void* q, const void* k, const void* v, const void* o, const float* lse,
-                       const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
+                       const void* dout, void* dq, void* dk, void* dv, void* workspace, size_t workspace_size,
                        int B, int Hq, int Hkv, int T, int D,
                        const int64_t* strides, float scale, int dtype,
                        const float* rope_cos, const float* rope_sin, void* stream);
 int mt_gqa_attn_bwd_dkv(const void* q, const void* k, const void* v, const void* o, const float* lse,
-                        const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
+                        const void* dout, void* dq, void* dk, void* dv, void* workspace, size_t workspace_size,
                         int B, int Hq, int Hkv, int T, int D,
                         const int64_t* strides, float scale, int dtype,
                         const float* rope_cos, const float* rope_sin, void* stream);

@@ -21,6 +21,7 @@ DTYPE_FP16 = 1
 EXPORTS = (
     "mt_version",
     "mt_last_error",
+    "mt_gqa_attn_bwd_workspace_size",
     "mt_gqa_attn_fwd",
     "mt_gqa_attn_bwd",
     "mt_gqa_attn_bwd_dq",
@@ -33,8 +34,9 @@ _lib: ctypes.CDLL | None = None
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
-_FWD_ARGTYPES = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
-_BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
+_S = ctypes.c_size_t
+_FWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
+_BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
 
 
 class HipAttentionError(RuntimeError):
@@ -63,6 +65,8 @@ def load() -> ctypes.CDLL:
         lib.mt_version.argtypes = []
         lib.mt_last_error.restype = ctypes.c_char_p
         lib.mt_last_error.argtypes = []
+        lib.mt_gqa_attn_bwd_workspace_size.restype = _S
+        lib.mt_gqa_attn_bwd_workspace_size.argtypes = [_I, _I, _I, _I, _I]
         lib.mt_gqa_attn_fwd.restype = _I
         lib.mt_gqa_attn_fwd.argtypes = _FWD_ARGTYPES
         for name in ("mt_gqa_attn_bwd", "mt_gqa_attn_bwd_dq", "mt_gqa_attn_bwd_dkv"):

@@ -158,42 +158,65 @@ def _forward(q, k, v, cos, sin):
         o, lse = _forward(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), cos, sin)
         return o.to(torch.float32), lse
     scale = 1.0 / math.sqrt(q.shape[-1])
-    return torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, v, cos, sin, scale)
+    if cos is None:
+        return torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, v, scale)
+    out, lse, _q_rot, _k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(q, k, v, cos, sin, scale)
+    return out, lse
+
+
+def _launch_fwd(q, k, v, cos, sin, scale):
+    lib = _native.load()
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    b, hq, t, d = q.shape
+    hkv = k.shape[1]
+    out = _kernel_ready(torch.empty_like(q))
+    lse = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
+    q_rot = k_rot = None
+    if cos is not None:
+        q_rot = torch.empty((b, hq, t, d), device=q.device, dtype=q.dtype)
+        k_rot = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
+    strides = _strides(q, k, v, out)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = lib.mt_gqa_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(), _ptr(q_rot), _ptr(k_rot),
+            b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
+        )
+    _native.check(rc, "mt_gqa_attn_fwd")
+    return out, lse, q_rot, k_rot
 
 
 # ---------------------------------------------------------------------------
 # custom ops
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("mega_trading_amd::gqa_attn_fwd", mutates_args=(), device_types="cuda")
-def gqa_attn_fwd(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    cos: Optional[torch.Tensor],
-    sin: Optional[torch.Tensor],
-    scale: float,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    lib = _native.load()
-    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-    b, hq, t, d = q.shape
-    hkv = k.shape[1]
-    out = torch.empty_like(q)
-    out = _kernel_ready(out)
-    lse = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
-    strides = _strides(q, k, v, out)
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = lib.mt_gqa_attn_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-            b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
-        )
-    _native.check(rc, "mt_gqa_attn_fwd")
+def gqa_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    out, lse, _, _ = _launch_fwd(q, k, v, None, None, scale)
     return out, lse
 
 
 @gqa_attn_fwd.register_fake
-def _gqa_attn_fwd_fake(q, k, v, cos, sin, scale):
+def _gqa_attn_fwd_fake(q, k, v, scale):
     return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
+
+
+@torch.library.custom_op("mega_trading_amd::gqa_rope_attn_fwd", mutates_args=(), device_types="cuda")
+def gqa_rope_attn_fwd(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, scale: float
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns (out, lse, q_rot, k_rot); q_rot/k_rot feed the backward."""
+    return _launch_fwd(q, k, v, cos, sin, scale)
+
+
+@gqa_rope_attn_fwd.register_fake
+def _gqa_rope_attn_fwd_fake(q, k, v, cos, sin, scale):
+    b, hq, t, d = q.shape
+    return (
+        torch.empty_like(q),
+        q.new_empty((b, hq, t), dtype=torch.float32),
+        q.new_empty((b, hq, t, d)),
+        q.new_empty((b, k.shape[1], t, d)),
+    )
 
 
 @torch.library.custom_op("mega_trading_amd::gqa_attn_bwd", mutates_args=(), device_types="cuda")
@@ -208,22 +231,25 @@ def gqa_attn_bwd(
     sin: Optional[torch.Tensor],
     scale: float,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients w.r.t. (q, k, v).  With RoPE tables, q and k are the rotated
+    tensors of the forward and dQ/dK come back in the un-rotated basis."""
     lib = _native.load()
     q, k, v, o = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(o)
     dout = _kernel_ready(dout.to(q.dtype))
     lse = lse.contiguous()
     b, hq, t, d = q.shape
     hkv = k.shape[1]
-    dq = _kernel_ready(torch.empty_like(q))
-    dk = _kernel_ready(torch.empty_like(k))
-    dv = _kernel_ready(torch.empty_like(v))
-    delta = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
+    dq = torch.empty((b, hq, t, d), device=q.device, dtype=q.dtype)
+    dk = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
+    dv = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
     strides = _strides(q, k, v, o, dout, dq, dk, dv)
     with torch.cuda.device(q.device):
+        ws_bytes = lib.mt_gqa_attn_bwd_workspace_size(b, hq, hkv, t, d)
+        workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
         stream = torch.cuda.current_stream(q.device).cuda_stream
         rc = lib.mt_gqa_attn_bwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dout.data_ptr(),
-            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), workspace.data_ptr(), ws_bytes,
             b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
         )
     _native.check(rc, "mt_gqa_attn_bwd")
@@ -232,21 +258,38 @@ def gqa_attn_bwd(
 
 @gqa_attn_bwd.register_fake
 def _gqa_attn_bwd_fake(q, k, v, o, lse, dout, cos, sin, scale):
-    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
 
 
 def _fwd_setup_context(ctx, inputs, output):
-    q, k, v, cos, sin, scale = inputs
+    q, k, v, scale = inputs
     out, lse = output
-    ctx.save_for_backward(q, k, v, out, lse, cos, sin)
+    ctx.save_for_backward(q, k, v, out, lse)
     ctx.scale = scale
     ctx.mark_non_differentiable(lse)
+    ctx.set_materialize_grads(False)
 
 
 def _fwd_backward(ctx, grad_out, _grad_lse):
-    q, k, v, out, lse, cos, sin = ctx.saved_tensors
-    dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q, k, v, out, lse, grad_out, cos, sin, ctx.scale)
+    q, k, v, out, lse = ctx.saved_tensors
+    dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q, k, v, out, lse, grad_out, None, None, ctx.scale)
+    return dq, dk, dv, None
+
+
+def _rope_fwd_setup_context(ctx, inputs, output):
+    _q, _k, v, cos, sin, scale = inputs
+    out, lse, q_rot, k_rot = output
+    ctx.save_for_backward(q_rot, k_rot, v, out, lse, cos, sin)
+    ctx.scale = scale
+    ctx.mark_non_differentiable(lse, q_rot, k_rot)
+    ctx.set_materialize_grads(False)
+
+
+def _rope_fwd_backward(ctx, grad_out, _grad_lse, _grad_q_rot, _grad_k_rot):
+    q_rot, k_rot, v, out, lse, cos, sin = ctx.saved_tensors
+    dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q_rot, k_rot, v, out, lse, grad_out, cos, sin, ctx.scale)
     return dq, dk, dv, None, None, None
 
 
 gqa_attn_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
+gqa_rope_attn_fwd.register_autograd(_rope_fwd_backward, setup_context=_rope_fwd_setup_context)

@@ -7,9 +7,13 @@
 //                       dQ = scale dS K)
 //   dK/dV    :618-747  (per KV block, loop over the group's query heads and the
 //                       causal row blocks; dV = P^T dO, dK = scale dS^T Q)
-// and the interleaved RoPE of src/mega_trading/model.py:312-316, fused into the
-// Q/K tile loads (the backward emits dQ/dK in the un-rotated basis, i.e. rotated
-// by -theta as src/mega_trading/kernels/triton_ops.py:205-214 does).
+// and the interleaved RoPE of src/mega_trading/model.py:312-316.
+//
+// RoPE.  The forward rotates each Q tile as it loads it into registers and
+// writes the rotated rows out (Q_rot); K is rotated once per call by a
+// streaming pass (K_rot) whose output feeds the forward's K tiles.  The
+// backward consumes Q_rot / K_rot directly and rotates dQ / dK back by -theta
+// in its epilogues (src/mega_trading/kernels/triton_ops.py:205-214).
 //
 // Tiling.  A "row block" is 64 query rows of one head, a "KV tile" 64 keys.
 //   * forward / dQ: a workgroup is 4 waves; each wave owns one (query head,
@@ -17,31 +21,36 @@
 //     times 4/R_SUB consecutive row blocks, so every K/V tile staged in LDS
 //     feeds all of them.  S^T = K Q^T puts one query per lane (lane % 32),
 //     keys along the accumulator slots; the row max needs one lane^32 swap.
-//   * dK/dV: a workgroup is 2 waves over 64 keys (32 keys each) of one KV head;
-//     it walks every (query head of the group, row block on or below the
-//     diagonal) and stages Q/dO in LDS once per step for both waves.
-// Fully masked causal tiles are never visited; only the diagonal tile masks.
+//   * dK/dV: a workgroup is 2 waves; each owns KPW keys of one KV head and
+//     walks (query head, row block on or below the diagonal) steps, with the
+//     Q / dO tiles of each step staged in LDS once for both waves.  The
+//     group's heads may be split over several workgroups (fp32 partial sums,
+//     combined by attn_bwd_combine_kernel) so the causal triangle spreads over
+//     enough workgroups to balance.
+// Fully masked causal tiles are never visited; only diagonal tiles mask.
 #pragma once
 
+#include "lds_tile.h"
 #include "mt_common.h"
 
 namespace mt {
 
 constexpr int kBlk = 64;   // rows per row block == keys per KV tile
-constexpr int kPad = 8;    // LDS row padding in 16-bit elements
 
 struct AttnParams {
   // [B, H, T, D] tensors, element strides (b, h, t); the d stride is 1.
-  const uint16_t* q;
-  const uint16_t* k;
+  const uint16_t* q;     // forward: un-rotated Q.  backward: the Q scores used (rotated if RoPE)
+  const uint16_t* k;     // forward: K (rotated if RoPE: the K_rot buffer).  backward: as for q
   const uint16_t* v;
   const uint16_t* o;
   const uint16_t* dout;
   uint16_t* out;   // forward: O.  backward: dQ
+  uint16_t* qrot;  // forward with RoPE: rotated Q out (contiguous [B,Hq,T,D])
   uint16_t* dk;
   uint16_t* dv;
   float* lse;      // [B, Hq, T] natural-log LSE (written by fwd, read by bwd)
   float* delta;    // [B, Hq, T] rowsum(O * dO) workspace (bwd)
+  float* part;     // [n_split, 2, B, Hkv, T, D] fp32 dK/dV partial sums (bwd, n_split > 1)
   const float* cos;  // [T, D/2] fp32 or null
   const float* sin;
   int64_t sq[3], sk[3], sv[3], so[3], sdo[3], sout[3], sdk[3], sdv[3];
@@ -51,13 +60,14 @@ struct AttnParams {
   int rb;         // row blocks per workgroup (4 / r_sub)
   int nqb;        // ceil(T / 64)
   int nsb;        // ceil(nqb / rb)
+  int n_split;    // dK/dV: workgroups sharing one key block (split of the R heads)
+  int nkb;        // dK/dV: key blocks
   float scale;       // softmax scale (1/sqrt(D) by default)
   float scale_log2;  // scale * log2(e)
 };
 
 // ---------------------------------------------------------------------------
-// Global -> register tile loads.  A "chunk" is 8 consecutive d values of one
-// row (16 bytes).  Rows at or beyond T read as zero.
+// small helpers
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ u32x4 load_chunk(const uint16_t* base, int64_t st, int row, int T, int d0) {
   if (row < T) return *reinterpret_cast<const u32x4*>(base + (int64_t)row * st + d0);
@@ -65,46 +75,9 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t* base, int64_t st, in
 }
 
 template <int D>
-__device__ __forceinline__ void load_rope_cs(const float* cos, const float* sin, int row, int T, int d0, f32x4& c, f32x4& s) {
-  if (row < T) {
-    c = *reinterpret_cast<const f32x4*>(cos + (int64_t)row * (D / 2) + d0 / 2);
-    s = *reinterpret_cast<const f32x4*>(sin + (int64_t)row * (D / 2) + d0 / 2);
-  } else {
-    c = f32x4{1.f, 1.f, 1.f, 1.f};
-    s = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-}
-
-// Write a chunk row-major: dst[row][d0..d0+7].
-template <int LD>
-__device__ __forceinline__ void st_row(uint16_t* dst, int row, int d0, u32x4 x) {
-  *reinterpret_cast<u32x4*>(dst + row * LD + d0) = x;
-}
-// Write a chunk transposed: dst[d0 + e][row] for e = 0..7.
-template <int LD>
-__device__ __forceinline__ void st_col(uint16_t* dst, int row, int d0, u32x4 x) {
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    dst[(d0 + 2 * p) * LD + row] = uint16_t(x[p] & 0xffffu);
-    dst[(d0 + 2 * p + 1) * LD + row] = uint16_t(x[p] >> 16);
-  }
-}
-
-// A operand read along a transposed tile: 8 slots = columns c0 + 4h + {0..3}
-// and c0 + 8 + 4h + {0..3} of row `row` (the permuted contraction order that
-// matches a C tile fed back as a B operand).
-template <class E, int LD>
-__device__ __forceinline__ typename E::v8 ld_perm(const uint16_t* src, int row, int c0, int h) {
-  const uint16_t* p = src + row * LD + c0 + 4 * h;
-  u32x2 lo = *reinterpret_cast<const u32x2*>(p);
-  u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
-  u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-  return __builtin_bit_cast(typename E::v8, w);
-}
-
-template <class E, int LD>
-__device__ __forceinline__ typename E::v8 ld_row8(const uint16_t* src, int row, int c0) {
-  return __builtin_bit_cast(typename E::v8, *reinterpret_cast<const u32x4*>(src + row * LD + c0));
+__device__ __forceinline__ void load_rope_cs(const float* cos, const float* sin, int row, int d0, f32x4& c, f32x4& s) {
+  c = *reinterpret_cast<const f32x4*>(cos + (int64_t)row * (D / 2) + d0 / 2);
+  s = *reinterpret_cast<const f32x4*>(sin + (int64_t)row * (D / 2) + d0 / 2);
 }
 
 // Pack C-tile slots [i0, i0+8) to an 8-wide 16-bit operand.
@@ -116,6 +89,20 @@ __device__ __forceinline__ typename E::v8 pack8(const f32x16& x, int i0) {
   return __builtin_bit_cast(typename E::v8, w);
 }
 
+__device__ __forceinline__ void zero16(f32x16& x) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = 0.f;
+}
+
+// Rotate 4 consecutive d values (2 interleaved pairs) by -theta in place.
+__device__ __forceinline__ void rope_back4(float& x0, float& x1, float& x2, float& x3, const float* cs, const float* sn) {
+  const f32x2 c = *reinterpret_cast<const f32x2*>(cs);
+  const f32x2 s = *reinterpret_cast<const f32x2*>(sn);
+  const float y0 = x0 * c[0] + x1 * s[0], y1 = x1 * c[0] - x0 * s[0];
+  const float y2 = x2 * c[1] + x3 * s[1], y3 = x3 * c[1] - x2 * s[1];
+  x0 = y0; x1 = y1; x2 = y2; x3 = y3;
+}
+
 // Workgroup -> (batch, kv head, head subset, super block) for fwd / dQ; the
 // longest causal rows are issued first.  Consecutive workgroups share a
 // (batch, kv head, subset) slot modulo the group count, so with a group count
@@ -124,32 +111,51 @@ struct RowTask {
   int b, kvh, hs, sb;
 };
 __device__ __forceinline__ RowTask row_task(const AttnParams& p) {
-  int groups = p.B * p.Hkv * p.n_hsub;
-  int L = blockIdx.x;
+  const int groups = p.B * p.Hkv * p.n_hsub;
+  const int L = blockIdx.x;
   RowTask t;
   t.sb = p.nsb - 1 - L / groups;
-  int g = L % groups;
+  const int g = L % groups;
   t.hs = g % p.n_hsub;
-  int bk = g / p.n_hsub;
+  const int bk = g / p.n_hsub;
   t.kvh = bk % p.Hkv;
   t.b = bk / p.Hkv;
   return t;
 }
 
 // ===========================================================================
+// RoPE streaming pass: Y = rot(X) for a [B, H, T, D] tensor, Y contiguous.
+// One thread per 16-byte chunk (4 interleaved pairs).
+// ===========================================================================
+template <class E, int D>
+__global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t* x, int64_t s0, int64_t s1, int64_t s2,
+                                                        uint16_t* y, const float* cos, const float* sin,
+                                                        int H, int T, int64_t n_chunks) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= n_chunks) return;
+  constexpr int NC = D / 8;
+  const int d0 = int(c % NC) * 8;
+  const int64_t row = c / NC;  // (b*H + h)*T + t
+  const int t = int(row % T);
+  const int64_t bh = row / T;
+  const int h = int(bh % H);
+  const int64_t b = bh / H;
+  u32x4 v = *reinterpret_cast<const u32x4*>(x + b * s0 + h * s1 + (int64_t)t * s2 + d0);
+  f32x4 cs, sn;
+  load_rope_cs<D>(cos, sin, t, d0, cs, sn);
+  *reinterpret_cast<u32x4*>(y + row * D + d0) = rope_chunk<E>(v, cs, sn);
+}
+
+// ===========================================================================
 // Forward
 // ===========================================================================
 template <class E, int D, bool ROPE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnParams p) {
   using V8 = typename E::v8;
+  using TL = Tile<D>;
   constexpr int KT = D / 16;            // k-steps over d
   constexpr int DT = D / 32;            // 32-wide d tiles
-  constexpr int LDK = D + kPad;         // Ks row stride
-  constexpr int LDV = kBlk + kPad;      // VsT row stride
-  constexpr int CH = kBlk * D / 8;      // chunks per tile
-  constexpr int CPT = CH / 256;         // chunks per thread
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBlk * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t VsT[2][D * LDV];
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
 
   const RowTask task = row_task(p);
   const int tid = threadIdx.x;
@@ -167,21 +173,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
   const uint16_t* kbase = p.k + task.b * p.sk[0] + (int64_t)task.kvh * p.sk[1];
   const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
 
-  // Q^T as B operands (N = query, k = d), rotated if RoPE.
+  // Q^T as B operands (N = query, k = d), rotated if RoPE (and written out).
   V8 qop[2][KT];
   {
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
+    uint16_t* rbase = ROPE ? p.qrot + ((int64_t)task.b * p.Hq + head) * p.T * D : nullptr;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int row = q0 + nt * 32 + l32;
+      const bool ok = active && row < p.T;
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
         const int d0 = 16 * kk + 8 * hh;
-        u32x4 x = active ? load_chunk(qbase, p.sq[2], row, p.T, d0) : zero4();
+        u32x4 x = ok ? load_chunk(qbase, p.sq[2], row, p.T, d0) : zero4();
         if constexpr (ROPE) {
-          f32x4 c, s;
-          load_rope_cs<D>(p.cos, p.sin, active ? row : p.T, p.T, d0, c, s);
-          x = rope_chunk<E>(x, c, s);
+          if (ok) {
+            f32x4 c, s;
+            load_rope_cs<D>(p.cos, p.sin, row, d0, c, s);
+            x = rope_chunk<E>(x, c, s);
+            *reinterpret_cast<u32x4*>(rbase + (int64_t)row * D + d0) = x;
+          }
         }
         qop[nt][kk] = __builtin_bit_cast(V8, x);
       }
@@ -192,63 +203,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[dt][nt][i] = 0.f;
+    for (int nt = 0; nt < 2; ++nt) zero16(oacc[dt][nt]);
   float mrun[2] = {-INFINITY, -INFINITY};
   float lrun[2] = {0.f, 0.f};
 
-  // staging registers (prefetch of the next KV tile)
-  u32x4 kreg[CPT], vreg[CPT];
-  f32x4 kc[CPT], ks[CPT];
-  auto fetch = [&](int j) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * 256;
-      const int row = c / (D / 8);
-      const int d0 = (c % (D / 8)) * 8;
-      const int key = j * kBlk + row;
-      kreg[i] = load_chunk(kbase, p.sk[2], key, p.T, d0);
-      vreg[i] = load_chunk(vbase, p.sv[2], key, p.T, d0);
-      if constexpr (ROPE) load_rope_cs<D>(p.cos, p.sin, key, p.T, d0, kc[i], ks[i]);
-    }
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * 256;
-      const int row = c / (D / 8);
-      const int d0 = (c % (D / 8)) * 8;
-      u32x4 x = kreg[i];
-      if constexpr (ROPE) x = rope_chunk<E>(x, kc[i], ks[i]);
-      st_row<LDK>(Ks[buf], row, d0, x);
-      st_col<LDV>(VsT[buf], row, d0, vreg[i]);
-    }
-  };
-
-  fetch(0);
-  commit(0);
+  TL::template stage<4>(smem[0][0], kbase, p.sk[2], 0, p.T, wave, lane);
+  TL::template stage<4>(smem[0][1], vbase, p.sv[2], 0, p.T, wave, lane);
+  wait_vmem();
   __syncthreads();
 
   const float c2 = p.scale_log2;
   for (int j = 0; j <= jlast; ++j) {
     const int buf = j & 1;
-    if (j < jlast) fetch(j + 1);
+    if (j < jlast) {
+      TL::template stage<4>(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T, wave, lane);
+      TL::template stage<4>(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T, wave, lane);
+    }
     if (active && j <= qb) {
-      const uint16_t* K = Ks[buf];
-      const uint16_t* Vt = VsT[buf];
+      const char* K = smem[buf][0];
+      const char* Vt = smem[buf][1];
       f32x16 st[2][2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) st[mt][nt][i] = 0.f;
+        for (int nt = 0; nt < 2; ++nt) zero16(st[mt][nt]);
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          V8 a = ld_row8<E, LDK>(K, mt * 32 + l32, 16 * kk + 8 * hh);
+          V8 a = TL::template row_op<E>(K, mt * 32, kk, lane);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][kk], st[mt][nt]);
         }
@@ -262,8 +245,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-              const int qr = nt * 32 + l32;
-              if (kr > qr) st[mt][nt][i] = -INFINITY;
+              if (kr > nt * 32 + l32) st[mt][nt][i] = -INFINITY;
             }
       }
       V8 pop[2][4];
@@ -299,13 +281,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          V8 a = ld_perm<E, LDV>(Vt, dt * 32 + l32, 16 * ks, hh);
+          V8 a = TL::template tr_op<E>(Vt, 16 * ks, dt * 32, lane);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pop[nt][ks], oacc[dt][nt]);
         }
       }
     }
-    if (j < jlast) commit(buf ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
@@ -336,17 +318,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
 // Backward, dQ (also writes delta = rowsum(O * dO))
 // ===========================================================================
 template <class E, int D, bool ROPE>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnParams p) {
   using V8 = typename E::v8;
+  using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  constexpr int LDK = D + kPad;      // Ks / Vs row stride
-  constexpr int LDT = kBlk + kPad;   // KsT row stride
-  constexpr int CH = kBlk * D / 8;
-  constexpr int CPT = CH / 256;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBlk * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBlk * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t KsT[2][D * LDT];
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
 
   const RowTask task = row_task(p);
   const int tid = threadIdx.x;
@@ -378,15 +355,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
         const int d0 = 16 * kk + 8 * hh;
-        u32x4 x = ok ? load_chunk(qbase, p.sq[2], row, p.T, d0) : zero4();
-        if constexpr (ROPE) {
-          f32x4 c, s;
-          load_rope_cs<D>(p.cos, p.sin, ok ? row : p.T, p.T, d0, c, s);
-          x = rope_chunk<E>(x, c, s);
-        }
-        qop[nt][kk] = __builtin_bit_cast(V8, x);
-        u32x4 g = ok ? load_chunk(gbase, p.sdo[2], row, p.T, d0) : zero4();
-        u32x4 o = ok ? load_chunk(obase, p.so[2], row, p.T, d0) : zero4();
+        qop[nt][kk] = __builtin_bit_cast(V8, ok ? load_chunk(qbase, p.sq[2], row, p.T, d0) : zero4());
+        const u32x4 g = ok ? load_chunk(gbase, p.sdo[2], row, p.T, d0) : zero4();
+        const u32x4 o = ok ? load_chunk(obase, p.so[2], row, p.T, d0) : zero4();
         gop[nt][kk] = __builtin_bit_cast(V8, g);
 #pragma unroll
         for (int w = 0; w < 4; ++w)
@@ -403,91 +374,69 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dqacc[dt][nt][i] = 0.f;
+    for (int nt = 0; nt < 2; ++nt) zero16(dqacc[dt][nt]);
 
-  u32x4 kreg[CPT], vreg[CPT];
-  f32x4 kc[CPT], ksn[CPT];
-  auto fetch = [&](int j) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * 256;
-      const int row = c / (D / 8);
-      const int d0 = (c % (D / 8)) * 8;
-      const int key = j * kBlk + row;
-      kreg[i] = load_chunk(kbase, p.sk[2], key, p.T, d0);
-      vreg[i] = load_chunk(vbase, p.sv[2], key, p.T, d0);
-      if constexpr (ROPE) load_rope_cs<D>(p.cos, p.sin, key, p.T, d0, kc[i], ksn[i]);
-    }
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * 256;
-      const int row = c / (D / 8);
-      const int d0 = (c % (D / 8)) * 8;
-      u32x4 x = kreg[i];
-      if constexpr (ROPE) x = rope_chunk<E>(x, kc[i], ksn[i]);
-      st_row<LDK>(Ks[buf], row, d0, x);
-      st_col<LDT>(KsT[buf], row, d0, x);
-      st_row<LDK>(Vs[buf], row, d0, vreg[i]);
-    }
-  };
-
-  fetch(0);
-  commit(0);
+  TL::template stage<4>(smem[0][0], kbase, p.sk[2], 0, p.T, wave, lane);
+  TL::template stage<4>(smem[0][1], vbase, p.sv[2], 0, p.T, wave, lane);
+  wait_vmem();
   __syncthreads();
 
   const float c2 = p.scale_log2;
   for (int j = 0; j <= jlast; ++j) {
     const int buf = j & 1;
-    if (j < jlast) fetch(j + 1);
+    if (j < jlast) {
+      TL::template stage<4>(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T, wave, lane);
+      TL::template stage<4>(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T, wave, lane);
+    }
     if (active && j <= qb) {
-      const uint16_t* K = Ks[buf];
-      const uint16_t* Vr = Vs[buf];
-      const uint16_t* Kt = KsT[buf];
+      const char* K = smem[buf][0];
+      const char* Vr = smem[buf][1];
+      f32x16 st[2][2], dpt[2][2];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        f32x16 st[2], dpt[2];
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int nt = 0; nt < 2; ++nt) { zero16(st[mt][nt]); zero16(dpt[mt][nt]); }
 #pragma unroll
-          for (int i = 0; i < 16; ++i) { st[mt][i] = 0.f; dpt[mt][i] = 0.f; }
+      for (int kk = 0; kk < KT; ++kk) {
 #pragma unroll
-        for (int kk = 0; kk < KT; ++kk) {
+        for (int mt = 0; mt < 2; ++mt) {
+          const V8 a = TL::template row_op<E>(K, mt * 32, kk, lane);
+          const V8 b = TL::template row_op<E>(Vr, mt * 32, kk, lane);
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            V8 a = ld_row8<E, LDK>(K, mt * 32 + l32, 16 * kk + 8 * hh);
-            st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
-            V8 b = ld_row8<E, LDK>(Vr, mt * 32 + l32, 16 * kk + 8 * hh);
-            dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
+          for (int nt = 0; nt < 2; ++nt) {
+            st[mt][nt] = E::mfma(a, qop[nt][kk], st[mt][nt]);
+            dpt[mt][nt] = E::mfma(b, gop[nt][kk], dpt[mt][nt]);
           }
         }
-        const int qr = nt * 32 + l32;
+      }
+      V8 dsb[2][4];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
+            float pv = exp2_fast(__builtin_fmaf(st[mt][nt][i], c2, -lse2[nt]));
             if (j == qb) {
               const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-              if (kr > qr) pv = 0.f;
+              if (kr > nt * 32 + l32) pv = 0.f;
             }
-            st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
+            st[mt][nt][i] = pv * (dpt[mt][nt][i] - dlt[nt]);
           }
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          V8 b = pack8<E>(st[ks >> 1], (ks & 1) * 8);
+        for (int ks = 0; ks < 4; ++ks) dsb[nt][ks] = pack8<E>(st[ks >> 1][nt], (ks & 1) * 8);
+      }
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            V8 a = ld_perm<E, LDT>(Kt, dt * 32 + l32, 16 * ks, hh);
-            dqacc[dt][nt] = E::mfma(a, b, dqacc[dt][nt]);
-          }
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const V8 a = TL::template tr_op<E>(K, 16 * ks, dt * 32, lane);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) dqacc[dt][nt] = E::mfma(a, dsb[nt][ks], dqacc[dt][nt]);
         }
       }
     }
-    if (j < jlast) commit(buf ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
@@ -504,16 +453,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
         const int d = dt * 32 + 8 * g + 4 * hh;
         float x0 = dqacc[dt][nt][4 * g] * p.scale, x1 = dqacc[dt][nt][4 * g + 1] * p.scale;
         float x2 = dqacc[dt][nt][4 * g + 2] * p.scale, x3 = dqacc[dt][nt][4 * g + 3] * p.scale;
-        if constexpr (ROPE) {
-          // rotate back by -theta: (e, o) -> (e c + o s, -e s + o c)
-          const float* cp = p.cos + (int64_t)row * (D / 2) + d / 2;
-          const float* sp = p.sin + (int64_t)row * (D / 2) + d / 2;
-          f32x2 c = *reinterpret_cast<const f32x2*>(cp);
-          f32x2 s = *reinterpret_cast<const f32x2*>(sp);
-          float y0 = x0 * c[0] + x1 * s[0], y1 = x1 * c[0] - x0 * s[0];
-          float y2 = x2 * c[1] + x3 * s[1], y3 = x3 * c[1] - x2 * s[1];
-          x0 = y0; x1 = y1; x2 = y2; x3 = y3;
-        }
+        if constexpr (ROPE)
+          rope_back4(x0, x1, x2, x3, p.cos + (int64_t)row * (D / 2) + d / 2, p.sin + (int64_t)row * (D / 2) + d / 2);
         u32x2 w = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
         *reinterpret_cast<u32x2*>(dqbase + (int64_t)row * p.sout[2] + d) = w;
       }
@@ -523,203 +464,227 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
 // ===========================================================================
 // Backward, dK / dV
 // ===========================================================================
-constexpr int kKvWaves = 2;                 // waves per dK/dV workgroup
-constexpr int kKvKeys = 32 * kKvWaves;      // keys per dK/dV workgroup (== kBlk)
-static_assert(kKvKeys == kBlk, "dK/dV key block must equal the row block");
+constexpr int kKvWaves = 2;  // waves per dK/dV workgroup
+
+template <int D>
+struct KvShape {
+  static constexpr int KPW = D <= 64 ? 64 : 32;  // keys per wave
+  static constexpr int KEYS = KPW * kKvWaves;    // keys per workgroup
+};
 
 template <class E, int D, bool ROPE>
-__global__ __launch_bounds__(64 * kKvWaves, 2) void attn_bwd_dkv_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kKvWaves, 1) void attn_bwd_dkv_kernel(AttnParams p) {
   using V8 = typename E::v8;
-  constexpr int NT = 64 * kKvWaves;
+  using TL = Tile<D>;
+  constexpr int KPW = KvShape<D>::KPW;
+  constexpr int KEYS = KvShape<D>::KEYS;
+  constexpr int NKT = KPW / 32;  // 32-key N tiles per wave
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  constexpr int LDR = D + kPad;      // row-major Q / dO stride
-  constexpr int LDT = kBlk + kPad;   // transposed Q^T / dO^T stride
-  constexpr int CH = kBlk * D / 8;
-  constexpr int CPT = CH / NT;
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][kBlk * LDR];
-  __shared__ __attribute__((aligned(16))) uint16_t Gs[2][kBlk * LDR];
-  __shared__ __attribute__((aligned(16))) uint16_t QsT[2][D * LDT];
-  __shared__ __attribute__((aligned(16))) uint16_t GsT[2][D * LDT];
-  __shared__ __attribute__((aligned(16))) float Ls[2][kBlk];
-  __shared__ __attribute__((aligned(16))) float Ds[2][kBlk];
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][Q, dO]
+  __shared__ __attribute__((aligned(16))) float vec[2][2][kBlk];         // [buf][lse, delta]
 
   // heaviest key blocks (smallest index: most causal rows) first
-  const int groups = p.B * p.Hkv;
+  const int groups = p.B * p.Hkv * p.n_split;
   const int L = blockIdx.x;
   const int kb = L / groups;
   const int g = L % groups;
-  const int kvh = g % p.Hkv;
-  const int b = g / p.Hkv;
+  const int hs = g % p.n_split;
+  const int bk = g / p.n_split;
+  const int kvh = bk % p.Hkv;
+  const int b = bk / p.Hkv;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  const int k0 = kb * kBlk + wave * 32;     // this wave's first key
-  const int key = k0 + l32;                 // this lane's key (C column)
+  const int k0 = kb * KEYS + wave * KPW;   // this wave's first key
+  const bool wave_live = k0 < p.T;
 
   // K and V rows as B operands (N = key, k = d)
-  V8 kop[KT], vop[KT];
+  V8 kop[NKT][KT], vop[NKT][KT];
   {
     const uint16_t* kbase = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1];
     const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1];
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      const int d0 = 16 * kk + 8 * hh;
-      u32x4 x = load_chunk(kbase, p.sk[2], key, p.T, d0);
-      if constexpr (ROPE) {
-        f32x4 c, s;
-        load_rope_cs<D>(p.cos, p.sin, key, p.T, d0, c, s);
-        x = rope_chunk<E>(x, c, s);
+    for (int nt = 0; nt < NKT; ++nt)
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        const int key = k0 + nt * 32 + l32;
+        const int d0 = 16 * kk + 8 * hh;
+        kop[nt][kk] = __builtin_bit_cast(V8, load_chunk(kbase, p.sk[2], key, p.T, d0));
+        vop[nt][kk] = __builtin_bit_cast(V8, load_chunk(vbase, p.sv[2], key, p.T, d0));
       }
-      kop[kk] = __builtin_bit_cast(V8, x);
-      vop[kk] = __builtin_bit_cast(V8, load_chunk(vbase, p.sv[2], key, p.T, d0));
-    }
   }
 
-  f32x16 dkacc[DT], dvacc[DT];
+  f32x16 dkacc[DT][NKT], dvacc[DT][NKT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { dkacc[dt][i] = 0.f; dvacc[dt][i] = 0.f; }
+    for (int nt = 0; nt < NKT; ++nt) { zero16(dkacc[dt][nt]); zero16(dvacc[dt][nt]); }
 
-  const int nblk_q = p.nqb - kb;          // row blocks on or below the diagonal
-  const int n_it = p.R * nblk_q;
+  const int hpt = p.R / p.n_split;                 // heads per task
+  const int qb0 = (kb * KEYS) / kBlk;              // first row block touching these keys
+  const int nblk_q = p.nqb - qb0;
+  const int n_it = hpt * nblk_q;
 
-  u32x4 qreg[CPT], greg[CPT];
-  f32x4 qc[CPT], qs[CPT];
-  float lreg = 0.f, dreg = 0.f;
-  auto fetch = [&](int it) {
-    const int r = it / nblk_q;
-    const int qb = kb + it % nblk_q;
-    const int head = kvh * p.R + r;
+  auto stage = [&](int it, int buf) {
+    const int head = kvh * p.R + hs * hpt + it / nblk_q;
+    const int qb = qb0 + it % nblk_q;
     const uint16_t* qbase = p.q + b * p.sq[0] + (int64_t)head * p.sq[1];
     const uint16_t* gbase = p.dout + b * p.sdo[0] + (int64_t)head * p.sdo[1];
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * NT;
-      const int row = c / (D / 8);
-      const int d0 = (c % (D / 8)) * 8;
-      const int t = qb * kBlk + row;
-      qreg[i] = load_chunk(qbase, p.sq[2], t, p.T, d0);
-      greg[i] = load_chunk(gbase, p.sdo[2], t, p.T, d0);
-      if constexpr (ROPE) load_rope_cs<D>(p.cos, p.sin, t, p.T, d0, qc[i], qs[i]);
-    }
-    if (tid < kBlk) {
-      const int t = qb * kBlk + tid;
-      const int64_t rb = ((int64_t)b * p.Hq + head) * p.T;
-      lreg = t < p.T ? p.lse[rb + t] * kLog2e : 0.f;
-      dreg = t < p.T ? p.delta[rb + t] : 0.f;
-    }
-  };
-  auto commit = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * NT;
-      const int row = c / (D / 8);
-      const int d0 = (c % (D / 8)) * 8;
-      u32x4 x = qreg[i];
-      if constexpr (ROPE) x = rope_chunk<E>(x, qc[i], qs[i]);
-      st_row<LDR>(Qs[buf], row, d0, x);
-      st_col<LDT>(QsT[buf], row, d0, x);
-      st_row<LDR>(Gs[buf], row, d0, greg[i]);
-      st_col<LDT>(GsT[buf], row, d0, greg[i]);
-    }
-    if (tid < kBlk) {
-      Ls[buf][tid] = lreg;
-      Ds[buf][tid] = dreg;
-    }
+    TL::template stage<kKvWaves>(smem[buf][0], qbase, p.sq[2], qb * kBlk, p.T, wave, lane);
+    TL::template stage<kKvWaves>(smem[buf][1], gbase, p.sdo[2], qb * kBlk, p.T, wave, lane);
+    const int64_t rb = ((int64_t)b * p.Hq + head) * p.T;
+    if (wave == 0) stage_vec64(reinterpret_cast<char*>(vec[buf][0]), p.lse + rb, qb * kBlk, p.T, lane);
+    else stage_vec64(reinterpret_cast<char*>(vec[buf][1]), p.delta + rb, qb * kBlk, p.T, lane);
   };
 
-  fetch(0);
-  commit(0);
+  stage(0, 0);
+  wait_vmem();
   __syncthreads();
 
   const float c2 = p.scale_log2;
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
-    if (it + 1 < n_it) fetch(it + 1);
-    const int qb = kb + it % nblk_q;
-    const int qbase_row = qb * kBlk;
-    {
-      const uint16_t* Q = Qs[buf];
-      const uint16_t* G = Gs[buf];
-      const uint16_t* Qt = QsT[buf];
-      const uint16_t* Gt = GsT[buf];
-      V8 pop[4], dsop[4];
+    if (it + 1 < n_it) stage(it + 1, buf ^ 1);
+    const int qrow0 = (qb0 + it % nblk_q) * kBlk;
+    // skip when every key of this wave lies after every query row of the block
+    if (wave_live && k0 <= qrow0 + kBlk - 1) {
+      const char* Q = smem[buf][0];
+      const char* G = smem[buf][1];
+      V8 pop[4][NKT], dsop[4][NKT];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        f32x16 s, dp;
+        f32x16 s[NKT], dp[NKT];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) { s[i] = 0.f; dp[i] = 0.f; }
+        for (int nt = 0; nt < NKT; ++nt) { zero16(s[nt]); zero16(dp[nt]); }
 #pragma unroll
         for (int kk = 0; kk < KT; ++kk) {
-          V8 a = ld_row8<E, LDR>(Q, mt * 32 + l32, 16 * kk + 8 * hh);
-          s = E::mfma(a, kop[kk], s);
-          V8 a2 = ld_row8<E, LDR>(G, mt * 32 + l32, 16 * kk + 8 * hh);
-          dp = E::mfma(a2, vop[kk], dp);
+          const V8 a = TL::template row_op<E>(Q, mt * 32, kk, lane);
+          const V8 a2 = TL::template row_op<E>(G, mt * 32, kk, lane);
+#pragma unroll
+          for (int nt = 0; nt < NKT; ++nt) {
+            s[nt] = E::mfma(a, kop[nt][kk], s[nt]);
+            dp[nt] = E::mfma(a2, vop[nt][kk], dp[nt]);
+          }
         }
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int qr = mt * 32 + 8 * g4 + 4 * hh;   // first of 4 query rows in these slots
-          f32x4 l4 = *reinterpret_cast<const f32x4*>(&Ls[buf][qr]);
-          f32x4 d4 = *reinterpret_cast<const f32x4*>(&Ds[buf][qr]);
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&vec[buf][0][qr]);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&vec[buf][1][qr]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = 4 * g4 + e;
-            const int qg = qbase_row + qr + e;
-            float pv = exp2_fast(__builtin_fmaf(s[i], c2, -l4[e]));
-            if (key > qg || qg >= p.T) pv = 0.f;
-            s[i] = pv;
-            dp[i] = pv * (dp[i] - d4[e]);
+            const int qg = qrow0 + qr + e;
+#pragma unroll
+            for (int nt = 0; nt < NKT; ++nt) {
+              const int key = k0 + nt * 32 + l32;
+              float pv = exp2_fast(__builtin_fmaf(s[nt][i], c2, -l4[e] * kLog2e));
+              if (key > qg || qg >= p.T) pv = 0.f;
+              s[nt][i] = pv;
+              dp[nt][i] = pv * (dp[nt][i] - d4[e]);
+            }
           }
         }
-        pop[2 * mt] = pack8<E>(s, 0);
-        pop[2 * mt + 1] = pack8<E>(s, 8);
-        dsop[2 * mt] = pack8<E>(dp, 0);
-        dsop[2 * mt + 1] = pack8<E>(dp, 8);
+#pragma unroll
+        for (int nt = 0; nt < NKT; ++nt) {
+          pop[2 * mt][nt] = pack8<E>(s[nt], 0);
+          pop[2 * mt + 1][nt] = pack8<E>(s[nt], 8);
+          dsop[2 * mt][nt] = pack8<E>(dp[nt], 0);
+          dsop[2 * mt + 1][nt] = pack8<E>(dp[nt], 8);
+        }
       }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          V8 a = ld_perm<E, LDT>(Gt, dt * 32 + l32, 16 * ks, hh);
-          dvacc[dt] = E::mfma(a, pop[ks], dvacc[dt]);
-          V8 a2 = ld_perm<E, LDT>(Qt, dt * 32 + l32, 16 * ks, hh);
-          dkacc[dt] = E::mfma(a2, dsop[ks], dkacc[dt]);
+          const V8 a = TL::template tr_op<E>(G, 16 * ks, dt * 32, lane);
+          const V8 a2 = TL::template tr_op<E>(Q, 16 * ks, dt * 32, lane);
+#pragma unroll
+          for (int nt = 0; nt < NKT; ++nt) {
+            dvacc[dt][nt] = E::mfma(a, pop[ks][nt], dvacc[dt][nt]);
+            dkacc[dt][nt] = E::mfma(a2, dsop[ks][nt], dkacc[dt][nt]);
+          }
         }
       }
     }
-    if (it + 1 < n_it) commit(buf ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
-  if (key >= p.T) return;
-  uint16_t* dkbase = p.dk + b * p.sdk[0] + (int64_t)kvh * p.sdk[1] + (int64_t)key * p.sdk[2];
-  uint16_t* dvbase = p.dv + b * p.sdv[0] + (int64_t)kvh * p.sdv[1] + (int64_t)key * p.sdv[2];
+  if (!wave_live) return;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int nt = 0; nt < NKT; ++nt) {
+    const int key = k0 + nt * 32 + l32;
+    if (key >= p.T) continue;
+    if (p.n_split == 1) {
+      uint16_t* dkrow = p.dk + b * p.sdk[0] + (int64_t)kvh * p.sdk[1] + (int64_t)key * p.sdk[2];
+      uint16_t* dvrow = p.dv + b * p.sdv[0] + (int64_t)kvh * p.sdv[1] + (int64_t)key * p.sdv[2];
 #pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = dt * 32 + 8 * g4 + 4 * hh;
-      float x0 = dkacc[dt][4 * g4] * p.scale, x1 = dkacc[dt][4 * g4 + 1] * p.scale;
-      float x2 = dkacc[dt][4 * g4 + 2] * p.scale, x3 = dkacc[dt][4 * g4 + 3] * p.scale;
-      if constexpr (ROPE) {
-        const float* cp = p.cos + (int64_t)key * (D / 2) + d / 2;
-        const float* sp = p.sin + (int64_t)key * (D / 2) + d / 2;
-        f32x2 c = *reinterpret_cast<const f32x2*>(cp);
-        f32x2 s = *reinterpret_cast<const f32x2*>(sp);
-        float y0 = x0 * c[0] + x1 * s[0], y1 = x1 * c[0] - x0 * s[0];
-        float y2 = x2 * c[1] + x3 * s[1], y3 = x3 * c[1] - x2 * s[1];
-        x0 = y0; x1 = y1; x2 = y2; x3 = y3;
-      }
-      u32x2 wk = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
-      *reinterpret_cast<u32x2*>(dkbase + d) = wk;
-      u32x2 wv = {pack2<E>(dvacc[dt][4 * g4], dvacc[dt][4 * g4 + 1]), pack2<E>(dvacc[dt][4 * g4 + 2], dvacc[dt][4 * g4 + 3])};
-      *reinterpret_cast<u32x2*>(dvbase + d) = wv;
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = dt * 32 + 8 * g4 + 4 * hh;
+          float x0 = dkacc[dt][nt][4 * g4] * p.scale, x1 = dkacc[dt][nt][4 * g4 + 1] * p.scale;
+          float x2 = dkacc[dt][nt][4 * g4 + 2] * p.scale, x3 = dkacc[dt][nt][4 * g4 + 3] * p.scale;
+          if constexpr (ROPE)
+            rope_back4(x0, x1, x2, x3, p.cos + (int64_t)key * (D / 2) + d / 2, p.sin + (int64_t)key * (D / 2) + d / 2);
+          u32x2 wk = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
+          *reinterpret_cast<u32x2*>(dkrow + d) = wk;
+          u32x2 wv = {pack2<E>(dvacc[dt][nt][4 * g4], dvacc[dt][nt][4 * g4 + 1]),
+                      pack2<E>(dvacc[dt][nt][4 * g4 + 2], dvacc[dt][nt][4 * g4 + 3])};
+          *reinterpret_cast<u32x2*>(dvrow + d) = wv;
+        }
+    } else {
+      // fp32 partials: part[hs][0 = dK, 1 = dV][b][kvh][key][d]
+      const int64_t plane = (int64_t)p.B * p.Hkv * p.T * D;
+      float* pk = p.part + (int64_t)hs * 2 * plane + (((int64_t)b * p.Hkv + kvh) * p.T + key) * D;
+      float* pv = pk + plane;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = dt * 32 + 8 * g4 + 4 * hh;
+          f32x4 xk = {dkacc[dt][nt][4 * g4] * p.scale, dkacc[dt][nt][4 * g4 + 1] * p.scale,
+                      dkacc[dt][nt][4 * g4 + 2] * p.scale, dkacc[dt][nt][4 * g4 + 3] * p.scale};
+          f32x4 xv = {dvacc[dt][nt][4 * g4], dvacc[dt][nt][4 * g4 + 1], dvacc[dt][nt][4 * g4 + 2], dvacc[dt][nt][4 * g4 + 3]};
+          *reinterpret_cast<f32x4*>(pk + d) = xk;
+          *reinterpret_cast<f32x4*>(pv + d) = xv;
+        }
     }
+  }
+}
+
+// Sum the n_split fp32 partials, rotate dK back (RoPE) and store dK / dV.
+// One thread per 4 consecutive d values of one key row.
+template <class E, int D, bool ROPE>
+__global__ __launch_bounds__(256) void attn_bwd_combine_kernel(AttnParams p) {
+  const int64_t n4 = (int64_t)p.B * p.Hkv * p.T * (D / 4);
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= n4) return;
+  const int d = int(c % (D / 4)) * 4;
+  const int64_t row = c / (D / 4);  // (b*Hkv + kvh)*T + key
+  const int key = int(row % p.T);
+  const int64_t bk = row / p.T;
+  const int kvh = int(bk % p.Hkv);
+  const int64_t b = bk / p.Hkv;
+  const int64_t plane = (int64_t)p.B * p.Hkv * p.T * D;
+  f32x4 sk = {0.f, 0.f, 0.f, 0.f}, sv = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < p.n_split; ++s) {
+    const float* pk = p.part + (int64_t)s * 2 * plane + row * D + d;
+    sk += *reinterpret_cast<const f32x4*>(pk);
+    sv += *reinterpret_cast<const f32x4*>(pk + plane);
+  }
+  float x0 = sk[0], x1 = sk[1], x2 = sk[2], x3 = sk[3];
+  if constexpr (ROPE)
+    rope_back4(x0, x1, x2, x3, p.cos + (int64_t)key * (D / 2) + d / 2, p.sin + (int64_t)key * (D / 2) + d / 2);
+  u32x2 wk = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
+  u32x2 wv = {pack2<E>(sv[0], sv[1]), pack2<E>(sv[2], sv[3])};
+  *reinterpret_cast<u32x2*>(p.dk + b * p.sdk[0] + (int64_t)kvh * p.sdk[1] + (int64_t)key * p.sdk[2] + d) = wk;
+  *reinterpret_cast<u32x2*>(p.dv + b * p.sdv[0] + (int64_t)kvh * p.sdv[1] + (int64_t)key * p.sdv[2] + d) = wv;
 }
 
 }  // namespace mt

@@ -31,7 +31,7 @@ int ok() {
   return MT_OK;
 }
 
-// Strides for one [B,H,T,D] tensor: d stride must be 1 and rows 16-byte aligned.
+// One [B,H,T,D] tensor: d stride must be 1, rows 16-byte aligned.
 int check_tensor(const char* name, const void* ptr, const int64_t* s) {
   if (!ptr) return fail(MT_E_NULL, "%s is NULL", name);
   if (s[3] != 1) return fail(MT_E_STRIDE, "%s: last-dim stride must be 1 (got %lld)", name, (long long)s[3]);
@@ -52,7 +52,47 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, const float* c
   return MT_OK;
 }
 
-void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, float scale) {
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+int kv_keys(int D) { return D <= 64 ? mt::KvShape<64>::KEYS : mt::KvShape<128>::KEYS; }
+
+// How many workgroups share a key block in the dK/dV pass: the smallest
+// divisor of R that gives about four workgroups per CU (two resident per CU,
+// so two rounds), letting the heaviest-first order pair long and short
+// causal tasks.
+int choose_split(int B, int Hq, int Hkv, int T, int D) {
+  const int R = Hq / Hkv;
+  const int nkb = (T + kv_keys(D) - 1) / kv_keys(D);
+  const long tasks = (long)nkb * B * Hkv;
+  const long want = 4L * device_cus();
+  int split = 1;
+  for (int s = 1; s <= R; ++s) {
+    if (R % s) continue;
+    split = s;
+    if (tasks * s >= want) break;
+  }
+  return split;
+}
+
+size_t delta_bytes(int B, int Hq, int T) { return (((size_t)B * Hq * T * sizeof(float)) + 255) / 256 * 256; }
+
+size_t workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  const int split = choose_split(B, Hq, Hkv, T, D);
+  const size_t part = split > 1 ? (size_t)split * 2 * B * Hkv * T * D * sizeof(float) : 0;
+  return delta_bytes(B, Hq, T) + part;
+}
+
+void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, float scale) {
   p.B = B;
   p.Hq = Hq;
   p.Hkv = Hkv;
@@ -63,6 +103,8 @@ void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, float scale
   p.rb = 4 / p.r_sub;
   p.nqb = (T + mt::kBlk - 1) / mt::kBlk;
   p.nsb = (p.nqb + p.rb - 1) / p.rb;
+  p.nkb = (T + kv_keys(D) - 1) / kv_keys(D);
+  p.n_split = choose_split(B, Hq, Hkv, T, D);
   p.scale = scale;
   p.scale_log2 = scale * mt::kLog2e;
 }
@@ -74,7 +116,19 @@ void copy3(int64_t dst[3], const int64_t* s) {
 }
 
 template <class E, int D, bool ROPE>
-hipError_t launch_fwd(const mt::AttnParams& p, hipStream_t st) {
+hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
+  if (ROPE) {
+    // K_rot = rot(K), contiguous; the forward's K tiles and the backward read it
+    const int64_t chunks = (int64_t)p.B * p.Hkv * p.T * (D / 8);
+    hipLaunchKernelGGL((mt::rope_rows_kernel<E, D>), dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st,
+                       p.k, p.sk[0], p.sk[1], p.sk[2], p.dk, p.cos, p.sin, p.Hkv, p.T, chunks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    p.k = p.dk;
+    p.sk[0] = (int64_t)p.Hkv * p.T * D;
+    p.sk[1] = (int64_t)p.T * D;
+    p.sk[2] = D;
+  }
   dim3 grid(p.nsb * p.B * p.Hkv * p.n_hsub);
   hipLaunchKernelGGL((mt::attn_fwd_kernel<E, D, ROPE>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
@@ -82,7 +136,7 @@ hipError_t launch_fwd(const mt::AttnParams& p, hipStream_t st) {
 
 // stage: 1 = dQ (+ delta), 2 = dK/dV, 3 = both
 template <class E, int D, bool ROPE>
-hipError_t launch_bwd(const mt::AttnParams& p, hipStream_t st, int stage) {
+hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
   if (stage & 1) {
     dim3 grid_dq(p.nsb * p.B * p.Hkv * p.n_hsub);
     hipLaunchKernelGGL((mt::attn_bwd_dq_kernel<E, D, ROPE>), grid_dq, dim3(256), 0, st, p);
@@ -90,23 +144,24 @@ hipError_t launch_bwd(const mt::AttnParams& p, hipStream_t st, int stage) {
     if (e != hipSuccess) return e;
   }
   if (stage & 2) {
-    dim3 grid_kv(p.nqb * p.B * p.Hkv);
+    dim3 grid_kv(p.nkb * p.B * p.Hkv * p.n_split);
     hipLaunchKernelGGL((mt::attn_bwd_dkv_kernel<E, D, ROPE>), grid_kv, dim3(64 * mt::kKvWaves), 0, st, p);
-    return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (p.n_split > 1) {
+      const int64_t n4 = (int64_t)p.B * p.Hkv * p.T * (D / 4);
+      hipLaunchKernelGGL((mt::attn_bwd_combine_kernel<E, D, ROPE>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, p);
+      return hipGetLastError();
+    }
   }
   return hipSuccess;
 }
 
-template <class E, int D, bool ROPE>
-hipError_t launch_fwd_s(const mt::AttnParams& p, hipStream_t st, int) {
-  return launch_fwd<E, D, ROPE>(p, st);
-}
-
-using Launcher = hipError_t (*)(const mt::AttnParams&, hipStream_t, int);
+using Launcher = hipError_t (*)(mt::AttnParams, hipStream_t, int);
 
 template <bool FWD, class E, int D>
 Launcher pick_rope(bool rope) {
-  if (FWD) return rope ? &launch_fwd_s<E, D, true> : &launch_fwd_s<E, D, false>;
+  if (FWD) return rope ? &launch_fwd<E, D, true> : &launch_fwd<E, D, false>;
   return rope ? &launch_bwd<E, D, true> : &launch_bwd<E, D, false>;
 }
 
@@ -122,55 +177,19 @@ Launcher pick(int dtype, int D, bool rope) {
   return pick_rope<FWD, mt::FP16, 128>(rope);
 }
 
-}  // namespace
-
-extern "C" {
-
-int mt_version(void) { return (0 << 16) | 1; }
-
-const char* mt_last_error(void) { return g_err; }
-
-int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
-                    int B, int Hq, int Hkv, int T, int D,
-                    const int64_t* strides, float scale, int dtype,
-                    const float* rope_cos, const float* rope_sin, void* stream) {
+int bwd_impl(int stage, const void* q, const void* k, const void* v, const void* o, const float* lse,
+             const void* dout, void* dq, void* dk, void* dv, void* workspace, size_t workspace_size,
+             int B, int Hq, int Hkv, int T, int D, const int64_t* strides, float scale, int dtype,
+             const float* rope_cos, const float* rope_sin, void* stream) {
   int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
   if (rc) return rc;
   if (!strides) return fail(MT_E_NULL, "strides is NULL");
   if (!lse) return fail(MT_E_NULL, "lse is NULL");
-  if ((rc = check_tensor("q", q, strides + 0))) return rc;
-  if ((rc = check_tensor("k", k, strides + 4))) return rc;
-  if ((rc = check_tensor("v", v, strides + 8))) return rc;
-  if ((rc = check_tensor("o", o, strides + 12))) return rc;
-
-  mt::AttnParams p{};
-  p.q = static_cast<const uint16_t*>(q);
-  p.k = static_cast<const uint16_t*>(k);
-  p.v = static_cast<const uint16_t*>(v);
-  p.out = static_cast<uint16_t*>(o);
-  p.lse = lse;
-  p.cos = rope_cos;
-  p.sin = rope_sin;
-  copy3(p.sq, strides + 0);
-  copy3(p.sk, strides + 4);
-  copy3(p.sv, strides + 8);
-  copy3(p.so, strides + 12);
-  fill_geometry(p, B, Hq, Hkv, T, scale);
-  hipError_t e = pick<true>(dtype, D, rope_cos != nullptr)(p, static_cast<hipStream_t>(stream), 0);
-  if (e != hipSuccess) return fail(int(e), "forward launch failed: %s", hipGetErrorString(e));
-  return ok();
-}
-
-static int bwd_impl(int stage, const void* q, const void* k, const void* v, const void* o, const float* lse,
-                    const void* dout, void* dq, void* dk, void* dv, float* delta_ws,
-                    int B, int Hq, int Hkv, int T, int D,
-                    const int64_t* strides, float scale, int dtype,
-                    const float* rope_cos, const float* rope_sin, void* stream) {
-  int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
-  if (rc) return rc;
-  if (!strides) return fail(MT_E_NULL, "strides is NULL");
-  if (!lse) return fail(MT_E_NULL, "lse is NULL");
-  if (!delta_ws) return fail(MT_E_NULL, "delta_ws is NULL");
+  if (!workspace) return fail(MT_E_NULL, "workspace is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(MT_E_STRIDE, "workspace must be 256-byte aligned");
+  const size_t need = workspace_bytes(B, Hq, Hkv, T, D);
+  if (workspace_size < need)
+    return fail(MT_E_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", workspace_size, need);
   if ((rc = check_tensor("q", q, strides + 0))) return rc;
   if ((rc = check_tensor("k", k, strides + 4))) return rc;
   if ((rc = check_tensor("v", v, strides + 8))) return rc;
@@ -190,7 +209,8 @@ static int bwd_impl(int stage, const void* q, const void* k, const void* v, cons
   p.dk = static_cast<uint16_t*>(dk);
   p.dv = static_cast<uint16_t*>(dv);
   p.lse = const_cast<float*>(lse);
-  p.delta = delta_ws;
+  p.delta = static_cast<float*>(workspace);
+  p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes(B, Hq, T));
   p.cos = rope_cos;
   p.sin = rope_sin;
   copy3(p.sq, strides + 0);
@@ -201,19 +221,71 @@ static int bwd_impl(int stage, const void* q, const void* k, const void* v, cons
   copy3(p.sout, strides + 20);
   copy3(p.sdk, strides + 24);
   copy3(p.sdv, strides + 28);
-  fill_geometry(p, B, Hq, Hkv, T, scale);
+  fill_geometry(p, B, Hq, Hkv, T, D, scale);
   hipError_t e = pick<false>(dtype, D, rope_cos != nullptr)(p, static_cast<hipStream_t>(stream), stage);
   if (e != hipSuccess) return fail(int(e), "backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 
-#define MT_BWD_ARGS                                                                            \
-  const void *q, const void *k, const void *v, const void *o, const float *lse, const void *dout, \
-      void *dq, void *dk, void *dv, float *delta_ws, int B, int Hq, int Hkv, int T, int D,         \
-      const int64_t *strides, float scale, int dtype, const float *rope_cos, const float *rope_sin, \
-      void *stream
-#define MT_BWD_PASS \
-  q, k, v, o, lse, dout, dq, dk, dv, delta_ws, B, Hq, Hkv, T, D, strides, scale, dtype, rope_cos, rope_sin, stream
+}  // namespace
+
+extern "C" {
+
+int mt_version(void) { return (0 << 16) | 2; }
+
+const char* mt_last_error(void) { return g_err; }
+
+size_t mt_gqa_attn_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || T < 1 || Hq % Hkv) return 0;
+  return workspace_bytes(B, Hq, Hkv, T, D);
+}
+
+int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, void* q_rot, void* k_rot,
+                    int B, int Hq, int Hkv, int T, int D,
+                    const int64_t* strides, float scale, int dtype,
+                    const float* rope_cos, const float* rope_sin, void* stream) {
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
+  if (rc) return rc;
+  if (!strides) return fail(MT_E_NULL, "strides is NULL");
+  if (!lse) return fail(MT_E_NULL, "lse is NULL");
+  if ((rc = check_tensor("q", q, strides + 0))) return rc;
+  if ((rc = check_tensor("k", k, strides + 4))) return rc;
+  if ((rc = check_tensor("v", v, strides + 8))) return rc;
+  if ((rc = check_tensor("o", o, strides + 12))) return rc;
+  if (rope_cos) {
+    if (!q_rot || !k_rot) return fail(MT_E_NULL, "q_rot and k_rot are required with RoPE tables");
+    if (reinterpret_cast<uintptr_t>(q_rot) % 16 || reinterpret_cast<uintptr_t>(k_rot) % 16)
+      return fail(MT_E_STRIDE, "q_rot / k_rot must be 16-byte aligned");
+  }
+
+  mt::AttnParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.out = static_cast<uint16_t*>(o);
+  p.qrot = static_cast<uint16_t*>(q_rot);
+  p.dk = static_cast<uint16_t*>(k_rot);  // destination of the K RoPE pass
+  p.lse = lse;
+  p.cos = rope_cos;
+  p.sin = rope_sin;
+  copy3(p.sq, strides + 0);
+  copy3(p.sk, strides + 4);
+  copy3(p.sv, strides + 8);
+  copy3(p.so, strides + 12);
+  fill_geometry(p, B, Hq, Hkv, T, D, scale);
+  hipError_t e = pick<true>(dtype, D, rope_cos != nullptr)(p, static_cast<hipStream_t>(stream), 0);
+  if (e != hipSuccess) return fail(int(e), "forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+#define MT_BWD_ARGS                                                                                     \
+  const void *q, const void *k, const void *v, const void *o, const float *lse, const void *dout,      \
+      void *dq, void *dk, void *dv, void *workspace, size_t workspace_size, int B, int Hq, int Hkv,    \
+      int T, int D, const int64_t *strides, float scale, int dtype, const float *rope_cos,             \
+      const float *rope_sin, void *stream
+#define MT_BWD_PASS                                                                                     \
+  q, k, v, o, lse, dout, dq, dk, dv, workspace, workspace_size, B, Hq, Hkv, T, D, strides, scale, dtype, \
+      rope_cos, rope_sin, stream
 
 int mt_gqa_attn_bwd(MT_BWD_ARGS) { return bwd_impl(3, MT_BWD_PASS); }
 int mt_gqa_attn_bwd_dq(MT_BWD_ARGS) { return bwd_impl(1, MT_BWD_PASS); }

@@ -21,7 +21,7 @@ HEADER = os.path.join(ROOT, "include", "mt_attention.h")
 
 def _header_functions() -> list[str]:
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mt_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mt_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_exports_every_declared_symbol(mta):
@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(mta):
     assert declared == sorted(mta._native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/mt_attention.h but not exported"
-    assert lib.mt_version() == (0 << 16) | 1
+    assert lib.mt_version() == (0 << 16) | 2
 
 
 def test_library_is_gfx950_only(mta):
@@ -41,11 +41,11 @@ def test_library_is_gfx950_only(mta):
 
 
 def _fwd_call(lib, q=0x1000, k=0x1000, v=0x1000, o=0x1000, lse=0x1000, b=1, hq=4, hkv=2, t=16, d=64,
-              strides=None, dtype=0, cos=None, sin=None):
+              strides=None, dtype=0, cos=None, sin=None, qrot=None, krot=None):
     if strides is None:
         strides = [hq * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hq * t * d, t * d, d, 1]
     arr = (ctypes.c_int64 * 16)(*strides)
-    return lib.mt_gqa_attn_fwd(q, k, v, o, lse, b, hq, hkv, t, d, arr, 0.125, dtype, cos, sin, None)
+    return lib.mt_gqa_attn_fwd(q, k, v, o, lse, qrot, krot, b, hq, hkv, t, d, arr, 0.125, dtype, cos, sin, None)
 
 
 def test_c_abi_rejects_bad_arguments_before_launch(mta):
@@ -61,6 +61,8 @@ def test_c_abi_rejects_bad_arguments_before_launch(mta):
     assert _fwd_call(lib, dtype=7) == E_DTYPE
     assert _fwd_call(lib, cos=0x1000, sin=None) == E_ROPE
     assert _fwd_call(lib, cos=0x1008, sin=0x1008) == E_ROPE  # misaligned tables
+    assert _fwd_call(lib, cos=0x1000, sin=0x1000) == E_NULL  # RoPE needs q_rot / k_rot outputs
+    assert b"q_rot" in lib.mt_last_error()
     bad = [4 * 16 * 64, 16 * 64, 64, 2] + [2 * 16 * 64, 16 * 64, 64, 1] * 2 + [4 * 16 * 64, 16 * 64, 64, 1]
     assert _fwd_call(lib, strides=bad) == E_STRIDE
     assert b"last-dim stride" in lib.mt_last_error()
@@ -68,13 +70,21 @@ def test_c_abi_rejects_bad_arguments_before_launch(mta):
     assert _fwd_call(lib, strides=odd) == E_STRIDE
     assert _fwd_call(lib, q=0x1002) == E_STRIDE  # misaligned base
     arr = (ctypes.c_int64 * 32)(*([1] * 32))
-    assert lib.mt_gqa_attn_bwd(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, None,
+    p = 0x1000
+    assert lib.mt_gqa_attn_bwd(p, p, p, p, p, p, p, p, p, None, 1 << 20,
                                1, 4, 2, 16, 64, arr, 0.125, 0, None, None, None) == E_NULL
-    assert b"delta_ws" in lib.mt_last_error()
+    assert b"workspace" in lib.mt_last_error()
+    need = lib.mt_gqa_attn_bwd_workspace_size(1, 4, 2, 16, 64)
+    assert need >= 4 * 16 * 4  # at least delta = [B, Hq, T] fp32
+    assert lib.mt_gqa_attn_bwd_workspace_size(1, 5, 2, 16, 64) == 0
+    assert lib.mt_gqa_attn_bwd(p, p, p, p, p, p, p, p, p, p, need - 1,
+                               1, 4, 2, 16, 64, arr, 0.125, 0, None, None, None) == -6
+    assert b"workspace too small" in lib.mt_last_error()
+    assert lib.mt_gqa_attn_bwd(p, p, p, p, p, p, p, p, p, p + 16, need,
+                               1, 4, 2, 16, 64, arr, 0.125, 0, None, None, None) == E_STRIDE
     for name in ("mt_gqa_attn_bwd_dq", "mt_gqa_attn_bwd_dkv"):
         fn = getattr(lib, name)
-        assert fn(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 0x1000,
-                  1, 4, 2, 16, 33, arr, 0.125, 0, None, None, None) == E_SHAPE
+        assert fn(p, p, p, p, p, p, p, p, p, p, need, 1, 4, 2, 16, 33, arr, 0.125, 0, None, None, None) == E_SHAPE
 
 
 def test_error_codes_raise_python_errors(mta):
@@ -122,8 +132,11 @@ def test_validation_errors_on_device_tensors(mta):
 def test_fake_impls_give_shapes_for_tracing(mta):
     with FakeTensorMode():
         q, k = _fake((2, 8, 100, 64)), _fake((2, 2, 100, 64))
-        out, lse = torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, k, None, None, 0.125)
+        out, lse = torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, k, 0.125)
         assert out.shape == q.shape and lse.shape == (2, 8, 100) and lse.dtype == torch.float32
+        cs = torch.empty(100, 32, device="cuda")
+        out2, lse2, qr, kr = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(q, k, k, cs, cs, 0.125)
+        assert out2.shape == q.shape and qr.shape == q.shape and kr.shape == k.shape
         dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q, k, k, out, lse, q, None, None, 0.125)
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
 
