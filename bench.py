@@ -198,6 +198,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="profiling driver: run only the C3 kernels stage by stage, then a 256 MiB device copy "
+                         "(the reference kernel for HBM-traffic counter calibration), and print their timings")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path is single-GPU; got --gpus {args.gpus})", file=sys.stderr)
@@ -207,6 +210,16 @@ def main(argv=None) -> int:
         return 2
     pkg = importlib.import_module("mega-trading_amd")
     pkg._native.load()
+
+    if args.kernels_only:
+        kern = time_kernels(pkg, C3, args.steps)
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernels": kern, "copy_bytes_each_way": 256 << 20}), flush=True)
+        return 0
 
     b, t, hq, hkv, d = C3
     ms_event, ms_wall = time_op_steps(pkg, C3, args.steps, args.warmup, rope=True)

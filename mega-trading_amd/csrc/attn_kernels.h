@@ -149,6 +149,13 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t* x, int64
 // ===========================================================================
 // Forward
 // ===========================================================================
+// Lazy rescaling: the running row max m used as the exponent offset is only
+// raised when a tile's max exceeds it by more than kRescaleSlack (log2
+// units), so P = 2^(s*c - m) stays below 2^kRescaleSlack and most tiles skip
+// the O / l rescale.  O = acc / l and LSE = (m + log2 l) * ln 2 are exact for
+// any m, so the result does not depend on when rescales happen.
+constexpr float kRescaleSlack = 8.0f;
+
 template <class E, int D, bool ROPE>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnParams p) {
   using V8 = typename E::v8;
@@ -207,8 +214,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   float mrun[2] = {-INFINITY, -INFINITY};
   float lrun[2] = {0.f, 0.f};
 
-  TL::template stage<4>(smem[0][0], kbase, p.sk[2], 0, p.T, wave, lane);
-  TL::template stage<4>(smem[0][1], vbase, p.sv[2], 0, p.T, wave, lane);
+  Stager<D, 4> ks_stage, vs_stage;
+  ks_stage.init(p.sk[2], wave, lane);
+  vs_stage.init(p.sv[2], wave, lane);
+  const int rbase_op = TL::row_base(lane);
+  const int tbase_op = TL::tr_base(lane);
+
+  ks_stage.stage(smem[0][0], kbase, p.sk[2], 0, p.T);
+  vs_stage.stage(smem[0][1], vbase, p.sv[2], 0, p.T);
   wait_vmem();
   __syncthreads();
 
@@ -216,22 +229,24 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   for (int j = 0; j <= jlast; ++j) {
     const int buf = j & 1;
     if (j < jlast) {
-      TL::template stage<4>(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T, wave, lane);
-      TL::template stage<4>(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T, wave, lane);
+      ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
+      vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
     }
     if (active && j <= qb) {
       const char* K = smem[buf][0];
       const char* Vt = smem[buf][1];
       f32x16 st[2][2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt) {
+        const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) zero16(st[mt][nt]);
+        for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][0], f32x16{});
+      }
 #pragma unroll
-      for (int kk = 0; kk < KT; ++kk) {
+      for (int kk = 1; kk < KT; ++kk) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          V8 a = TL::template row_op<E>(K, mt * 32, kk, lane);
+          const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, kk);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][kk], st[mt][nt]);
         }
@@ -257,23 +272,28 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
 #pragma unroll
           for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[mt][nt][i]);
         mx = max_with_partner(mx) * c2;
-        const float mnew = fmaxf(mrun[nt], mx);
-        const float alpha = exp2_fast(mrun[nt] - mnew);
-        mrun[nt] = mnew;
-        float ls = 0.f;
+        // wave-uniform: rescale only if some row's max outgrew its offset
+        if (__builtin_amdgcn_ballot_w64(mx > mrun[nt] + kRescaleSlack)) {
+          const float mnew = fmaxf(mrun[nt], mx);
+          const float alpha = exp2_fast(mrun[nt] - mnew);
+          mrun[nt] = mnew;
+          lrun[nt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
+        }
+        const float moff = mrun[nt];
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const float pv = exp2_fast(__builtin_fmaf(st[mt][nt][i], c2, -mnew));
+            const float pv = exp2_fast(__builtin_fmaf(st[mt][nt][i], c2, -moff));
             st[mt][nt][i] = pv;
-            ls += pv;
+            ls[i & 3] += pv;
           }
-        lrun[nt] = lrun[nt] * alpha + ls;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
+        lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) pop[nt][ks] = pack8<E>(st[ks >> 1][nt], (ks & 1) * 8);
       }
@@ -281,7 +301,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          V8 a = TL::template tr_op<E>(Vt, 16 * ks, dt * 32, lane);
+          const V8 a = TL::template tr_op<E>(Vt, tbase_op, ks, dt);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pop[nt][ks], oacc[dt][nt]);
         }
@@ -318,7 +338,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
 // Backward, dQ (also writes delta = rowsum(O * dO))
 // ===========================================================================
 template <class E, int D, bool ROPE>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
@@ -376,8 +396,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnParams p) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) zero16(dqacc[dt][nt]);
 
-  TL::template stage<4>(smem[0][0], kbase, p.sk[2], 0, p.T, wave, lane);
-  TL::template stage<4>(smem[0][1], vbase, p.sv[2], 0, p.T, wave, lane);
+  Stager<D, 4> ks_stage, vs_stage;
+  ks_stage.init(p.sk[2], wave, lane);
+  vs_stage.init(p.sv[2], wave, lane);
+  const int rbase_op = TL::row_base(lane);
+  const int tbase_op = TL::tr_base(lane);
+
+  ks_stage.stage(smem[0][0], kbase, p.sk[2], 0, p.T);
+  vs_stage.stage(smem[0][1], vbase, p.sv[2], 0, p.T);
   wait_vmem();
   __syncthreads();
 
@@ -385,55 +411,59 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnParams p) {
   for (int j = 0; j <= jlast; ++j) {
     const int buf = j & 1;
     if (j < jlast) {
-      TL::template stage<4>(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T, wave, lane);
-      TL::template stage<4>(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T, wave, lane);
+      ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
+      vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
     }
     if (active && j <= qb) {
       const char* K = smem[buf][0];
       const char* Vr = smem[buf][1];
-      f32x16 st[2][2], dpt[2][2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) { zero16(st[mt][nt]); zero16(dpt[mt][nt]); }
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const V8 a = TL::template row_op<E>(K, mt * 32, kk, lane);
-          const V8 b = TL::template row_op<E>(Vr, mt * 32, kk, lane);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            st[mt][nt] = E::mfma(a, qop[nt][kk], st[mt][nt]);
-            dpt[mt][nt] = E::mfma(b, gop[nt][kk], dpt[mt][nt]);
-          }
-        }
-      }
-      V8 dsb[2][4];
+      // the two 32-query halves one after the other keeps S/dP at 64 VGPRs
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
+        f32x16 st[2], dpt[2];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 2; ++mt) {
+          const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
+          const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, 0);
+          st[mt] = E::mfma(a, qop[nt][0], f32x16{});
+          dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
+        }
+#pragma unroll
+        for (int kk = 1; kk < KT; ++kk) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, kk);
+            const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, kk);
+            st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
+            dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
+          }
+        }
+        V8 dsb[4];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            float pv = exp2_fast(__builtin_fmaf(st[mt][nt][i], c2, -lse2[nt]));
+            float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
             if (j == qb) {
               const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
               if (kr > nt * 32 + l32) pv = 0.f;
             }
-            st[mt][nt][i] = pv * (dpt[mt][nt][i] - dlt[nt]);
+            st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
           }
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) dsb[nt][ks] = pack8<E>(st[ks >> 1][nt], (ks & 1) * 8);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const V8 a = TL::template tr_op<E>(K, 16 * ks, dt * 32, lane);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) dqacc[dt][nt] = E::mfma(a, dsb[nt][ks], dqacc[dt][nt]);
+          dsb[2 * mt] = pack8<E>(st[mt], 0);
+          dsb[2 * mt + 1] = pack8<E>(st[mt], 8);
         }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const V8 a = TL::template tr_op<E>(K, tbase_op, ks, dt);
+            dqacc[dt][nt] = E::mfma(a, dsb[ks], dqacc[dt][nt]);
+          }
+        }
+        // keep the two halves' live ranges apart (the scheduler would
+        // otherwise interleave them and exceed the register budget)
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_vmem();
@@ -464,21 +494,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnParams p) {
 // ===========================================================================
 // Backward, dK / dV
 // ===========================================================================
-constexpr int kKvWaves = 2;  // waves per dK/dV workgroup
-
-template <int D>
-struct KvShape {
-  static constexpr int KPW = D <= 64 ? 64 : 32;  // keys per wave
-  static constexpr int KEYS = KPW * kKvWaves;    // keys per workgroup
-};
+constexpr int kKvWaves = 4;   // waves per dK/dV workgroup
+constexpr int kKvKpw = 32;    // keys per wave
+constexpr int kKvKeys = kKvWaves * kKvKpw;
 
 template <class E, int D, bool ROPE>
-__global__ __launch_bounds__(64 * kKvWaves, 1) void attn_bwd_dkv_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
-  constexpr int KPW = KvShape<D>::KPW;
-  constexpr int KEYS = KvShape<D>::KEYS;
-  constexpr int NKT = KPW / 32;  // 32-key N tiles per wave
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
   __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][Q, dO]
@@ -499,46 +522,46 @@ __global__ __launch_bounds__(64 * kKvWaves, 1) void attn_bwd_dkv_kernel(AttnPara
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  const int k0 = kb * KEYS + wave * KPW;   // this wave's first key
+  const int k0 = kb * kKvKeys + wave * kKvKpw;   // this wave's first key
+  const int key = k0 + l32;                      // this lane's key (C column)
   const bool wave_live = k0 < p.T;
 
   // K and V rows as B operands (N = key, k = d)
-  V8 kop[NKT][KT], vop[NKT][KT];
+  V8 kop[KT], vop[KT];
   {
     const uint16_t* kbase = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1];
     const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1];
 #pragma unroll
-    for (int nt = 0; nt < NKT; ++nt)
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) {
-        const int key = k0 + nt * 32 + l32;
-        const int d0 = 16 * kk + 8 * hh;
-        kop[nt][kk] = __builtin_bit_cast(V8, load_chunk(kbase, p.sk[2], key, p.T, d0));
-        vop[nt][kk] = __builtin_bit_cast(V8, load_chunk(vbase, p.sv[2], key, p.T, d0));
-      }
+    for (int kk = 0; kk < KT; ++kk) {
+      const int d0 = 16 * kk + 8 * hh;
+      kop[kk] = __builtin_bit_cast(V8, load_chunk(kbase, p.sk[2], key, p.T, d0));
+      vop[kk] = __builtin_bit_cast(V8, load_chunk(vbase, p.sv[2], key, p.T, d0));
+    }
   }
 
-  f32x16 dkacc[DT][NKT], dvacc[DT][NKT];
+  f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int nt = 0; nt < NKT; ++nt) { zero16(dkacc[dt][nt]); zero16(dvacc[dt][nt]); }
+  for (int dt = 0; dt < DT; ++dt) { zero16(dkacc[dt]); zero16(dvacc[dt]); }
 
   const int hpt = p.R / p.n_split;                 // heads per task
-  const int qb0 = (kb * KEYS) / kBlk;              // first row block touching these keys
+  const int qb0 = (kb * kKvKeys) / kBlk;           // first row block touching these keys
   const int nblk_q = p.nqb - qb0;
   const int n_it = hpt * nblk_q;
+
+  Stager<D, kKvWaves> qs_stage, gs_stage;
+  qs_stage.init(p.sq[2], wave, lane);
+  gs_stage.init(p.sdo[2], wave, lane);
+  const int rbase_op = TL::row_base(lane);
+  const int tbase_op = TL::tr_base(lane);
 
   auto stage = [&](int it, int buf) {
     const int head = kvh * p.R + hs * hpt + it / nblk_q;
     const int qb = qb0 + it % nblk_q;
-    const uint16_t* qbase = p.q + b * p.sq[0] + (int64_t)head * p.sq[1];
-    const uint16_t* gbase = p.dout + b * p.sdo[0] + (int64_t)head * p.sdo[1];
-    TL::template stage<kKvWaves>(smem[buf][0], qbase, p.sq[2], qb * kBlk, p.T, wave, lane);
-    TL::template stage<kKvWaves>(smem[buf][1], gbase, p.sdo[2], qb * kBlk, p.T, wave, lane);
+    qs_stage.stage(smem[buf][0], p.q + b * p.sq[0] + (int64_t)head * p.sq[1], p.sq[2], qb * kBlk, p.T);
+    gs_stage.stage(smem[buf][1], p.dout + b * p.sdo[0] + (int64_t)head * p.sdo[1], p.sdo[2], qb * kBlk, p.T);
     const int64_t rb = ((int64_t)b * p.Hq + head) * p.T;
     if (wave == 0) stage_vec64(reinterpret_cast<char*>(vec[buf][0]), p.lse + rb, qb * kBlk, p.T, lane);
-    else stage_vec64(reinterpret_cast<char*>(vec[buf][1]), p.delta + rb, qb * kBlk, p.T, lane);
+    if (wave == 1) stage_vec64(reinterpret_cast<char*>(vec[buf][1]), p.delta + rb, qb * kBlk, p.T, lane);
   };
 
   stage(0, 0);
@@ -550,111 +573,90 @@ __global__ __launch_bounds__(64 * kKvWaves, 1) void attn_bwd_dkv_kernel(AttnPara
     const int buf = it & 1;
     if (it + 1 < n_it) stage(it + 1, buf ^ 1);
     const int qrow0 = (qb0 + it % nblk_q) * kBlk;
-    // skip when every key of this wave lies after every query row of the block
-    if (wave_live && k0 <= qrow0 + kBlk - 1) {
-      const char* Q = smem[buf][0];
-      const char* G = smem[buf][1];
-      V8 pop[4][NKT], dsop[4][NKT];
+    const char* Q = smem[buf][0];
+    const char* G = smem[buf][1];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        f32x16 s[NKT], dp[NKT];
-#pragma unroll
-        for (int nt = 0; nt < NKT; ++nt) { zero16(s[nt]); zero16(dp[nt]); }
-#pragma unroll
-        for (int kk = 0; kk < KT; ++kk) {
-          const V8 a = TL::template row_op<E>(Q, mt * 32, kk, lane);
-          const V8 a2 = TL::template row_op<E>(G, mt * 32, kk, lane);
-#pragma unroll
-          for (int nt = 0; nt < NKT; ++nt) {
-            s[nt] = E::mfma(a, kop[nt][kk], s[nt]);
-            dp[nt] = E::mfma(a2, vop[nt][kk], dp[nt]);
-          }
-        }
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int qr = mt * 32 + 8 * g4 + 4 * hh;   // first of 4 query rows in these slots
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&vec[buf][0][qr]);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&vec[buf][1][qr]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 4 * g4 + e;
-            const int qg = qrow0 + qr + e;
-#pragma unroll
-            for (int nt = 0; nt < NKT; ++nt) {
-              const int key = k0 + nt * 32 + l32;
-              float pv = exp2_fast(__builtin_fmaf(s[nt][i], c2, -l4[e] * kLog2e));
-              if (key > qg || qg >= p.T) pv = 0.f;
-              s[nt][i] = pv;
-              dp[nt][i] = pv * (dp[nt][i] - d4[e]);
-            }
-          }
-        }
-#pragma unroll
-        for (int nt = 0; nt < NKT; ++nt) {
-          pop[2 * mt][nt] = pack8<E>(s[nt], 0);
-          pop[2 * mt + 1][nt] = pack8<E>(s[nt], 8);
-          dsop[2 * mt][nt] = pack8<E>(dp[nt], 0);
-          dsop[2 * mt + 1][nt] = pack8<E>(dp[nt], 8);
-        }
+    for (int mt = 0; mt < 2; ++mt) {
+      // skip a 32-row half whose rows all precede every key of this wave
+      if (!wave_live || k0 > qrow0 + mt * 32 + 31) continue;
+      f32x16 s, dp;
+      {
+        const V8 a = TL::template row_op<E>(Q, rbase_op, mt * 32, 0);
+        const V8 a2 = TL::template row_op<E>(G, rbase_op, mt * 32, 0);
+        s = E::mfma(a, kop[0], f32x16{});
+        dp = E::mfma(a2, vop[0], f32x16{});
       }
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int kk = 1; kk < KT; ++kk) {
+        const V8 a = TL::template row_op<E>(Q, rbase_op, mt * 32, kk);
+        const V8 a2 = TL::template row_op<E>(G, rbase_op, mt * 32, kk);
+        s = E::mfma(a, kop[kk], s);
+        dp = E::mfma(a2, vop[kk], dp);
+      }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const V8 a = TL::template tr_op<E>(G, 16 * ks, dt * 32, lane);
-          const V8 a2 = TL::template tr_op<E>(Q, 16 * ks, dt * 32, lane);
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int qr = mt * 32 + 8 * g4 + 4 * hh;   // first of 4 query rows in these slots
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&vec[buf][0][qr]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&vec[buf][1][qr]);
 #pragma unroll
-          for (int nt = 0; nt < NKT; ++nt) {
-            dvacc[dt][nt] = E::mfma(a, pop[ks][nt], dvacc[dt][nt]);
-            dkacc[dt][nt] = E::mfma(a2, dsop[ks][nt], dkacc[dt][nt]);
-          }
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g4 + e;
+          const int qg = qrow0 + qr + e;
+          float pv = exp2_fast(__builtin_fmaf(s[i], c2, -l4[e] * kLog2e));
+          if (key > qg || qg >= p.T) pv = 0.f;
+          s[i] = pv;
+          dp[i] = pv * (dp[i] - d4[e]);
         }
+      }
+      const V8 p0 = pack8<E>(s, 0), p1 = pack8<E>(s, 8);
+      const V8 d0 = pack8<E>(dp, 0), d1 = pack8<E>(dp, 8);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dvacc[dt] = E::mfma(TL::template tr_op<E>(G, tbase_op, 2 * mt, dt), p0, dvacc[dt]);
+        dkacc[dt] = E::mfma(TL::template tr_op<E>(Q, tbase_op, 2 * mt, dt), d0, dkacc[dt]);
+        dvacc[dt] = E::mfma(TL::template tr_op<E>(G, tbase_op, 2 * mt + 1, dt), p1, dvacc[dt]);
+        dkacc[dt] = E::mfma(TL::template tr_op<E>(Q, tbase_op, 2 * mt + 1, dt), d1, dkacc[dt]);
       }
     }
     wait_vmem();
     __syncthreads();
   }
 
-  if (!wave_live) return;
+  if (!wave_live || key >= p.T) return;
+  if (p.n_split == 1) {
+    uint16_t* dkrow = p.dk + b * p.sdk[0] + (int64_t)kvh * p.sdk[1] + (int64_t)key * p.sdk[2];
+    uint16_t* dvrow = p.dv + b * p.sdv[0] + (int64_t)kvh * p.sdv[1] + (int64_t)key * p.sdv[2];
 #pragma unroll
-  for (int nt = 0; nt < NKT; ++nt) {
-    const int key = k0 + nt * 32 + l32;
-    if (key >= p.T) continue;
-    if (p.n_split == 1) {
-      uint16_t* dkrow = p.dk + b * p.sdk[0] + (int64_t)kvh * p.sdk[1] + (int64_t)key * p.sdk[2];
-      uint16_t* dvrow = p.dv + b * p.sdv[0] + (int64_t)kvh * p.sdv[1] + (int64_t)key * p.sdv[2];
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = dt * 32 + 8 * g4 + 4 * hh;
+        float x0 = dkacc[dt][4 * g4] * p.scale, x1 = dkacc[dt][4 * g4 + 1] * p.scale;
+        float x2 = dkacc[dt][4 * g4 + 2] * p.scale, x3 = dkacc[dt][4 * g4 + 3] * p.scale;
+        if constexpr (ROPE)
+          rope_back4(x0, x1, x2, x3, p.cos + (int64_t)key * (D / 2) + d / 2, p.sin + (int64_t)key * (D / 2) + d / 2);
+        u32x2 wk = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
+        *reinterpret_cast<u32x2*>(dkrow + d) = wk;
+        u32x2 wv = {pack2<E>(dvacc[dt][4 * g4], dvacc[dt][4 * g4 + 1]),
+                    pack2<E>(dvacc[dt][4 * g4 + 2], dvacc[dt][4 * g4 + 3])};
+        *reinterpret_cast<u32x2*>(dvrow + d) = wv;
+      }
+  } else {
+    // fp32 partials: part[hs][0 = dK, 1 = dV][b][kvh][key][d]
+    const int64_t plane = (int64_t)p.B * p.Hkv * p.T * D;
+    float* pk = p.part + (int64_t)hs * 2 * plane + (((int64_t)b * p.Hkv + kvh) * p.T + key) * D;
+    float* pv = pk + plane;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d = dt * 32 + 8 * g4 + 4 * hh;
-          float x0 = dkacc[dt][nt][4 * g4] * p.scale, x1 = dkacc[dt][nt][4 * g4 + 1] * p.scale;
-          float x2 = dkacc[dt][nt][4 * g4 + 2] * p.scale, x3 = dkacc[dt][nt][4 * g4 + 3] * p.scale;
-          if constexpr (ROPE)
-            rope_back4(x0, x1, x2, x3, p.cos + (int64_t)key * (D / 2) + d / 2, p.sin + (int64_t)key * (D / 2) + d / 2);
-          u32x2 wk = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
-          *reinterpret_cast<u32x2*>(dkrow + d) = wk;
-          u32x2 wv = {pack2<E>(dvacc[dt][nt][4 * g4], dvacc[dt][nt][4 * g4 + 1]),
-                      pack2<E>(dvacc[dt][nt][4 * g4 + 2], dvacc[dt][nt][4 * g4 + 3])};
-          *reinterpret_cast<u32x2*>(dvrow + d) = wv;
-        }
-    } else {
-      // fp32 partials: part[hs][0 = dK, 1 = dV][b][kvh][key][d]
-      const int64_t plane = (int64_t)p.B * p.Hkv * p.T * D;
-      float* pk = p.part + (int64_t)hs * 2 * plane + (((int64_t)b * p.Hkv + kvh) * p.T + key) * D;
-      float* pv = pk + plane;
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d = dt * 32 + 8 * g4 + 4 * hh;
-          f32x4 xk = {dkacc[dt][nt][4 * g4] * p.scale, dkacc[dt][nt][4 * g4 + 1] * p.scale,
-                      dkacc[dt][nt][4 * g4 + 2] * p.scale, dkacc[dt][nt][4 * g4 + 3] * p.scale};
-          f32x4 xv = {dvacc[dt][nt][4 * g4], dvacc[dt][nt][4 * g4 + 1], dvacc[dt][nt][4 * g4 + 2], dvacc[dt][nt][4 * g4 + 3]};
-          *reinterpret_cast<f32x4*>(pk + d) = xk;
-          *reinterpret_cast<f32x4*>(pv + d) = xv;
-        }
-    }
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = dt * 32 + 8 * g4 + 4 * hh;
+        f32x4 xk = {dkacc[dt][4 * g4] * p.scale, dkacc[dt][4 * g4 + 1] * p.scale,
+                    dkacc[dt][4 * g4 + 2] * p.scale, dkacc[dt][4 * g4 + 3] * p.scale};
+        f32x4 xv = {dvacc[dt][4 * g4], dvacc[dt][4 * g4 + 1], dvacc[dt][4 * g4 + 2], dvacc[dt][4 * g4 + 3]};
+        *reinterpret_cast<f32x4*>(pk + d) = xk;
+        *reinterpret_cast<f32x4*>(pv + d) = xv;
+      }
   }
 }
 

@@ -1,8 +1,11 @@
 // LDS tiles of 64 rows x D 16-bit elements for the gfx950 attention kernels.
 //
-// Layout: rows are stored unpadded (2*D bytes); the 16-byte chunks of row r
-// are XOR-swizzled, chunk c living at slot c ^ (r % SW), so that the 8 lanes
-// reading one chunk column of 8 consecutive rows hit 8 different slots.
+// Layout: rows are stored unpadded (RB = 2*D bytes); the 16-byte chunks of
+// row r are XOR-swizzled, chunk c living at slot c ^ (r % SW), so that the 8
+// lanes reading one chunk column of 8 consecutive rows hit 8 different slots.
+// Because the swizzle is an XOR with bits the operand offsets never touch,
+// every operand address is a per-lane base computed once, XOR-ed with a
+// per-step constant, plus an immediate row offset.
 //
 // Staging uses global_load_lds_dwordx4: each lane of a wave copies 16 bytes
 // from its own global address straight into LDS at (wave base + 16 * lane),
@@ -35,55 +38,84 @@ template <int D>
 struct Tile {
   static constexpr int NC = D / 8;              // 16-byte chunks per row
   static constexpr int SW = NC < 8 ? NC : 8;    // swizzle period
-  static constexpr int ROW_BYTES = 2 * D;
-  static constexpr int BYTES = 64 * ROW_BYTES;  // one 64-row tile
-  static constexpr int INSTR = 64 * NC / 64;    // 1 KB wave instructions per tile
+  static constexpr int RB = 2 * D;              // row bytes
+  static constexpr int BYTES = 64 * RB;         // one 64-row tile
+  static constexpr int INSTR = NC;              // 1 KB wave instructions per tile (64 * NC * 16 B / 1 KB)
 
-  static __device__ __forceinline__ int chunk_off(int row, int chunk) {
-    return row * ROW_BYTES + ((chunk ^ (row % SW)) << 4);
+  // --- operand addressing -------------------------------------------------
+  // row_op base: lane (row = lane % 32, chunk = lane / 32) at r0 = 0, kk = 0.
+  static __device__ __forceinline__ int row_base(int lane) {
+    const int row = lane & 31;
+    const int chunk = lane >> 5;
+    return row * RB + ((chunk ^ (row % SW)) << 4);
   }
-  // byte offset of element (row, col); col must be a multiple of 4
-  static __device__ __forceinline__ int elem_off(int row, int col) {
-    return chunk_off(row, col >> 3) + ((col & 7) << 1);
-  }
-
-  // Stage rows [row0, row0+64) of a row-strided 16-bit matrix into `lds`
-  // (byte pointer to the tile).  The workgroup's NW waves split the INSTR
-  // instructions; `wave`/`lane` identify the caller.
-  template <int NW>
-  static __device__ __forceinline__ void stage(char* lds, const uint16_t* src, int64_t row_stride, int row0,
-                                               int T, int wave, int lane) {
-    static_assert(INSTR % NW == 0, "tile instructions must split evenly over the waves");
-#pragma unroll
-    for (int i = 0; i < INSTR / NW; ++i) {
-      const int f = (i * NW + wave) * 64 + lane;  // flat LDS chunk index
-      const int row = f / NC;
-      const int slot = f % NC;
-      const int chunk = slot ^ (row % SW);
-      const int grow = min(row0 + row, T - 1);
-      const uint16_t* g = src + (int64_t)grow * row_stride + chunk * 8;
-      __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)(lds + (i * NW + wave) * 1024), 16, 0, 0);
-    }
-  }
-
-  template <class E>
-  static __device__ __forceinline__ typename E::v8 row_op(const char* lds, int r0, int kk, int lane) {
-    const int row = r0 + (lane & 31);
-    const int chunk = 2 * kk + (lane >> 5);
-    return *reinterpret_cast<const typename E::v8*>(lds + chunk_off(row, chunk));
-  }
-
-  template <class E>
-  static __device__ __forceinline__ typename E::v8 tr_op(const char* lds, int r0, int c0, int lane) {
+  // tr_op base: lane's 8-byte source at r0 = 0, c0 = 0 (first of the two reads).
+  static __device__ __forceinline__ int tr_base(int lane) {
     const int g = lane >> 4;
     const int i = lane & 15;
-    const int col = c0 + 16 * (g & 1) + 4 * (i & 3);
-    const int row = r0 + 4 * (g >> 1) + (i >> 2);
-    i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(lds + elem_off(row, col)));
-    i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(lds + elem_off(row + 8, col)));
+    const int row = 4 * (g >> 1) + (i >> 2);
+    const int col = 16 * (g & 1) + 4 * (i & 3);
+    return row * RB + (((col >> 3) ^ (row % SW)) << 4) + ((col & 7) << 1);
+  }
+
+  template <class E>
+  static __device__ __forceinline__ typename E::v8 row_op(const char* lds, int base, int r0, int kk) {
+    return *reinterpret_cast<const typename E::v8*>(lds + (base ^ (32 * kk)) + r0 * RB);
+  }
+
+  template <class E>
+  static __device__ __forceinline__ typename E::v8 tr_op(const char* lds, int base, int ks, int dt) {
+    const char* p = lds + (base ^ (64 * dt)) + 16 * ks * RB;
+    i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
+    i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * RB));
     u32x4 w = {__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
                __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]};
     return __builtin_bit_cast(typename E::v8, w);
+  }
+};
+
+// Staging of one 64-row tile by the NW waves of a workgroup: per-lane source
+// offsets (elements, relative to the tile's first row) of the INSTR/NW wave
+// instructions this wave issues, computed once.
+__device__ __forceinline__ void lds_dma16(const uint16_t* g, char* l) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+template <int D, int NW>
+struct Stager {
+  using TL = Tile<D>;
+  static_assert(TL::INSTR % NW == 0, "tile instructions must split evenly over the waves");
+  static constexpr int N = TL::INSTR / NW;
+  int off[N];   // row * row_stride + chunk * 8
+  int row[N];
+  int chunk[N];
+  int lds_off;  // byte offset of this wave's first 1 KB block in the tile
+
+  __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int f = (i * NW + wave) * 64 + lane;  // flat LDS chunk index
+      row[i] = f / TL::NC;
+      chunk[i] = (f % TL::NC) ^ (row[i] % TL::SW);
+      off[i] = row[i] * (int)row_stride + chunk[i] * 8;
+    }
+    lds_off = wave * 1024;
+  }
+
+  // Stage rows [row0, row0 + 64) of the matrix at `src` (row stride as in init).
+  __device__ __forceinline__ void stage(char* lds, const uint16_t* src, int64_t row_stride, int row0, int T) const {
+    if (row0 + 64 <= T) {
+      const uint16_t* tile = src + (int64_t)row0 * row_stride;
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        lds_dma16(tile + off[i], lds + lds_off + i * NW * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int grow = min(row0 + row[i], T - 1);
+        lds_dma16(src + (int64_t)grow * row_stride + chunk[i] * 8, lds + lds_off + i * NW * 1024);
+      }
+    }
   }
 };
 

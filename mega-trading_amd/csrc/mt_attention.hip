@@ -38,6 +38,8 @@ int check_tensor(const char* name, const void* ptr, const int64_t* s) {
   if (reinterpret_cast<uintptr_t>(ptr) % 16) return fail(MT_E_STRIDE, "%s: base pointer must be 16-byte aligned", name);
   for (int i = 0; i < 3; ++i)
     if (s[i] % 8) return fail(MT_E_STRIDE, "%s: stride %d (%lld) must be a multiple of 8 elements", name, i, (long long)s[i]);
+  // tile staging keeps 64 rows of offsets in 32-bit registers
+  if (s[2] > (int64_t(1) << 24)) return fail(MT_E_STRIDE, "%s: row stride %lld too large", name, (long long)s[2]);
   return MT_OK;
 }
 
@@ -64,7 +66,7 @@ int device_cus() {
   return cached[dev];
 }
 
-int kv_keys(int D) { return D <= 64 ? mt::KvShape<64>::KEYS : mt::KvShape<128>::KEYS; }
+int kv_keys(int) { return mt::kKvKeys; }
 
 // How many workgroups share a key block in the dK/dV pass: the smallest
 // divisor of R that gives about four workgroups per CU (two resident per CU,
