@@ -105,7 +105,10 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True):
 
 
 def time_kernels(pkg, cfg, iters):
-    """Average duration of each kernel, HIP events recorded on its launch stream."""
+    """Average duration of each kernel stage, HIP events recorded on its launch stream.
+
+    The forward stage includes the 5 us K-RoPE pass and the dK/dV stage the
+    partial-sum combine pass that follows its kernel."""
     native = pkg._native
     lib = native.load()
     b, t, hq, hkv, d = cfg
@@ -140,16 +143,17 @@ def time_kernels(pkg, cfg, iters):
         for _, fn in stages:
             fn()
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(iters)]
-    for i in range(iters):
-        ev[i][0].record(stream)
-        for j, (_, fn) in enumerate(stages):
-            fn()
-            ev[i][j + 1].record(stream)
-    torch.cuda.synchronize()
+    # each stage launched `iters` times back to back between two events on the
+    # launch stream, so per-launch event overhead does not inflate the average
     out = {}
-    for j, (name, _) in enumerate(stages):
-        ms = sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(iters)) / iters
+    for name, fn in stages:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(iters):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / iters
         flops = KERNEL_FLOP_UNITS[name] * b * hq * d * pairs(t)
         out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flop": flops}
     return out

@@ -50,6 +50,7 @@ struct AttnParams {
   uint16_t* dv;
   float* lse;      // [B, Hq, T] natural-log LSE (written by fwd, read by bwd)
   float* delta;    // [B, Hq, T] rowsum(O * dO) workspace (bwd)
+  float* lse2;     // [B, Hq, T] LSE * log2(e) workspace (written by dQ, read by dK/dV)
   float* part;     // [n_split, 2, B, Hkv, T, D] fp32 dK/dV partial sums (bwd, n_split > 1)
   const float* cos;  // [T, D/2] fp32 or null
   const float* sin;
@@ -238,23 +239,24 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
       f32x16 st[2][2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
+        {
+          const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][0], f32x16{});
-      }
+          for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][0], f32x16{});
+        }
 #pragma unroll
-      for (int kk = 1; kk < KT; ++kk) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int kk = 1; kk < KT; ++kk) {
           const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, kk);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][kk], st[mt][nt]);
         }
       }
-      if (j == qb) {
-        // diagonal tile: key (row m of S^T) > query (col n) is masked
+      // The two 32-key halves: the softmax of half 0 overlaps the S MFMAs of
+      // half 1, and half 0's PV MFMAs overlap the softmax of half 1.
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 2; ++mt) {
+        if (j == qb) {
+          // diagonal tile: key (row m of S^T) > query (col n) is masked
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -262,48 +264,45 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
               const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
               if (kr > nt * 32 + l32) st[mt][nt][i] = -INFINITY;
             }
-      }
-      V8 pop[2][4];
+        }
+        V8 pop[2][2];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int nt = 0; nt < 2; ++nt) {
+          float mx = -INFINITY;
 #pragma unroll
           for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[mt][nt][i]);
-        mx = max_with_partner(mx) * c2;
-        // wave-uniform: rescale only if some row's max outgrew its offset
-        if (__builtin_amdgcn_ballot_w64(mx > mrun[nt] + kRescaleSlack)) {
-          const float mnew = fmaxf(mrun[nt], mx);
-          const float alpha = exp2_fast(mrun[nt] - mnew);
-          mrun[nt] = mnew;
-          lrun[nt] *= alpha;
+          mx = max_with_partner(mx) * c2;
+          // wave-uniform: rescale only if some row's max outgrew its offset
+          if (__builtin_amdgcn_ballot_w64(mx > mrun[nt] + kRescaleSlack)) {
+            const float mnew = fmaxf(mrun[nt], mx);
+            const float alpha = exp2_fast(mrun[nt] - mnew);
+            mrun[nt] = mnew;
+            lrun[nt] *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
+            for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
-        }
-        const float moff = mrun[nt];
-        float ls[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+              for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
+          }
+          const float moff = mrun[nt];
+          float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const float pv = exp2_fast(__builtin_fmaf(st[mt][nt][i], c2, -moff));
             st[mt][nt][i] = pv;
             ls[i & 3] += pv;
           }
-        lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+          lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+          pop[nt][0] = pack8<E>(st[mt][nt], 0);
+          pop[nt][1] = pack8<E>(st[mt][nt], 8);
+        }
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) pop[nt][ks] = pack8<E>(st[ks >> 1][nt], (ks & 1) * 8);
-      }
+        for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+          for (int dt = 0; dt < DT; ++dt) {
+            const V8 a = TL::template tr_op<E>(Vt, tbase_op, 2 * mt + k2, dt);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const V8 a = TL::template tr_op<E>(Vt, tbase_op, ks, dt);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pop[nt][ks], oacc[dt][nt]);
+            for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pop[nt][k2], oacc[dt][nt]);
+          }
         }
       }
     }
@@ -386,7 +385,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
       dsum = sum_with_partner(dsum);
       dlt[nt] = dsum;
       lse2[nt] = ok ? p.lse[rowbase + row] * kLog2e : 0.f;
-      if (ok && hh == 0) p.delta[rowbase + row] = dsum;
+      if (ok && hh == 0) {
+        p.delta[rowbase + row] = dsum;
+        p.lse2[rowbase + row] = lse2[nt];
+      }
     }
   }
 
@@ -423,24 +425,23 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
         f32x16 st[2], dpt[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
-          const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, 0);
-          st[mt] = E::mfma(a, qop[nt][0], f32x16{});
-          dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
-        }
+          {
+            const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
+            const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, 0);
+            st[mt] = E::mfma(a, qop[nt][0], f32x16{});
+            dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
+          }
 #pragma unroll
-        for (int kk = 1; kk < KT; ++kk) {
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
+          for (int kk = 1; kk < KT; ++kk) {
             const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, kk);
             const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, kk);
             st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
             dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
           }
         }
-        V8 dsb[4];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
+          V8 dsb[2];
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
@@ -450,15 +451,15 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
             }
             st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
           }
-          dsb[2 * mt] = pack8<E>(st[mt], 0);
-          dsb[2 * mt + 1] = pack8<E>(st[mt], 8);
-        }
+          dsb[0] = pack8<E>(st[mt], 0);
+          dsb[1] = pack8<E>(st[mt], 8);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+          for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const V8 a = TL::template tr_op<E>(K, tbase_op, ks, dt);
-            dqacc[dt][nt] = E::mfma(a, dsb[ks], dqacc[dt][nt]);
+            for (int dt = 0; dt < DT; ++dt) {
+              const V8 a = TL::template tr_op<E>(K, tbase_op, 2 * mt + k2, dt);
+              dqacc[dt][nt] = E::mfma(a, dsb[k2], dqacc[dt][nt]);
+            }
           }
         }
         // keep the two halves' live ranges apart (the scheduler would
@@ -491,12 +492,163 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
   }
 }
 
+
+// dK/dV softmax step for one 32-row quarter (C layout: lane = key, slots =
+// rows): P = 2^(S*c - lse2[row]), dS = P * (dP - delta[row]); packs P and dS
+// into the two 16-row B operands.  l_rows / d_rows point at the quarter's
+// lse2 / delta values offset by 4 * (lane / 32); slot group g reads rows
+// 8g .. 8g+3.  With MASK, entries whose key exceeds the row or whose row is
+// at or past T are zeroed (qrow = the quarter's first global row).
+template <class E, bool MASK>
+__device__ __forceinline__ void softmax_dS32(f32x16& s, f32x16& dp, const float* l_rows, const float* d_rows,
+                                             float c2, int key, int qrow, int T, int hh,
+                                             typename E::v8 pk[2], typename E::v8 dk[2]) {
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const f32x4 l4 = *reinterpret_cast<const f32x4*>(l_rows + 8 * g4);
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(d_rows + 8 * g4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * g4 + e;
+      float pv = exp2_fast(__builtin_fmaf(s[i], c2, -l4[e]));
+      if constexpr (MASK) {
+        const int qg = qrow + 8 * g4 + 4 * hh + e;
+        if (key > qg || qg >= T) pv = 0.f;
+      }
+      s[i] = pv;
+      dp[i] = pv * (dp[i] - d4[e]);
+    }
+  }
+  pk[0] = pack8<E>(s, 0);
+  pk[1] = pack8<E>(s, 8);
+  dk[0] = pack8<E>(dp, 0);
+  dk[1] = pack8<E>(dp, 8);
+}
+
 // ===========================================================================
 // Backward, dK / dV
 // ===========================================================================
-constexpr int kKvWaves = 4;   // waves per dK/dV workgroup
-constexpr int kKvKpw = 32;    // keys per wave
+constexpr int kKvWaves = 4;    // waves per dK/dV workgroup
+constexpr int kKvKpw = 32;     // keys per wave
 constexpr int kKvKeys = kKvWaves * kKvKpw;
+constexpr int kKvRows = 128;   // query rows staged per step (two row blocks)
+
+// One step of a wave: rows [qrow0, qrow0 + 128) of one head against the
+// wave's 32 keys.  Quarter h covers rows qrow0 + 32h.  MFMA / VALU pipeline
+// (issue order, phases fenced by sched_barrier, MFMAs interleaved with the
+// VALU work of the same phase):
+//   SdP0 | SdP1 + V0 | dVdK0 + SdP2 + V1 | dVdK1 + SdP3 + V2 | dVdK2 + V3 | dVdK3
+// where SdPh = S and dP of quarter h, Vh = its softmax / dS, dVdKh = its
+// dV and dK updates.  Quarters with every key above every row are skipped
+// (LIVE masks only matter on the diagonal, where MASK is set).
+template <class E, int D, bool MASK>
+__device__ __forceinline__ void dkv_step(const char* Q, const char* G, const float* lrow, const float* drow,
+                                         const typename E::v8* kop, const typename E::v8* vop,
+                                         f32x16* dkacc, f32x16* dvacc, int rbase, int tbase, int lane,
+                                         int key, int k0, int qrow0, int T, float c2) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+  const int hh = lane >> 5;
+  // quarter live: some key of the wave is <= the quarter's last row
+  bool live[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) live[h] = !MASK || (k0 <= qrow0 + 32 * h + 31);
+
+  auto sdp = [&](int h, f32x16& s, f32x16& dp) {
+    const char* Qh = Q + (h >> 1) * TL::BYTES;
+    const char* Gh = G + (h >> 1) * TL::BYTES;
+    const int r0 = 32 * (h & 1);
+    V8 aq = TL::template row_op<E>(Qh, rbase, r0, 0);
+    V8 ag = TL::template row_op<E>(Gh, rbase, r0, 0);
+    s = E::mfma(aq, kop[0], f32x16{});
+    dp = E::mfma(ag, vop[0], f32x16{});
+#pragma unroll
+    for (int kk = 1; kk < KT; ++kk) {
+      aq = TL::template row_op<E>(Qh, rbase, r0, kk);
+      ag = TL::template row_op<E>(Gh, rbase, r0, kk);
+      s = E::mfma(aq, kop[kk], s);
+      dp = E::mfma(ag, vop[kk], dp);
+    }
+  };
+  auto vh = [&](int h, f32x16& s, f32x16& dp, V8* pk, V8* dk) {
+    softmax_dS32<E, MASK>(s, dp, lrow + 32 * h + 4 * hh, drow + 32 * h + 4 * hh, c2, key, qrow0 + 32 * h, T, hh, pk, dk);
+  };
+  auto dvdk = [&](int h, const V8* pk, const V8* dk) {
+    const char* Qh = Q + (h >> 1) * TL::BYTES;
+    const char* Gh = G + (h >> 1) * TL::BYTES;
+    const int ks0 = 2 * (h & 1);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dvacc[dt] = E::mfma(TL::template tr_op<E>(Gh, tbase, ks0 + k2, dt), pk[k2], dvacc[dt]);
+        dkacc[dt] = E::mfma(TL::template tr_op<E>(Qh, tbase, ks0 + k2, dt), dk[k2], dkacc[dt]);
+      }
+  };
+  constexpr int NS = 2 * KT;   // S/dP MFMAs of a quarter
+  constexpr int NT = 4 * DT;   // dV/dK MFMAs of a quarter
+
+  f32x16 s[2], dp[2];          // ring of two quarters' S / dP
+  V8 pk[2][2], dk[2][2];       // ring of two quarters' packed P / dS
+  // phase 1: SdP0
+  if (live[0]) sdp(0, s[0], dp[0]);
+#pragma unroll
+  for (int i = 0; i < KT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // phase 2: SdP1 + V0
+  if (live[1]) sdp(1, s[1], dp[1]);
+  if (live[0]) vh(0, s[0], dp[0], pk[0], dk[0]);
+#pragma unroll
+  for (int i = 0; i < KT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // phases 3, 4: dVdK(h-2) + SdP(h) + V(h-1), h = 2, 3
+#pragma unroll
+  for (int h = 2; h < 4; ++h) {
+    if (live[h - 2]) dvdk(h - 2, pk[h & 1], dk[h & 1]);
+    if (live[h]) sdp(h, s[h & 1], dp[h & 1]);
+    if (live[h - 1]) vh(h - 1, s[(h - 1) & 1], dp[(h - 1) & 1], pk[(h - 1) & 1], dk[(h - 1) & 1]);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < KT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // phase 5: dVdK2 + V3
+  if (live[2]) dvdk(2, pk[0], dk[0]);
+  if (live[3]) vh(3, s[1], dp[1], pk[1], dk[1]);
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // phase 6: dVdK3
+  if (live[3]) dvdk(3, pk[1], dk[1]);
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+  (void)NS;
+}
 
 template <class E, int D, bool ROPE>
 __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_kernel(AttnParams p) {
@@ -504,8 +656,9 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][Q, dO]
-  __shared__ __attribute__((aligned(16))) float vec[2][2][kBlk];         // [buf][lse, delta]
+  // [buf][Q, dO] x 128 rows (two 64-row tiles back to back)
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];
+  __shared__ __attribute__((aligned(16))) float vec[2][2][kKvRows];  // [buf][lse * log2(e), delta]
 
   // heaviest key blocks (smallest index: most causal rows) first
   const int groups = p.B * p.Hkv * p.n_split;
@@ -544,9 +697,9 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   for (int dt = 0; dt < DT; ++dt) { zero16(dkacc[dt]); zero16(dvacc[dt]); }
 
   const int hpt = p.R / p.n_split;                 // heads per task
-  const int qb0 = (kb * kKvKeys) / kBlk;           // first row block touching these keys
-  const int nblk_q = p.nqb - qb0;
-  const int n_it = hpt * nblk_q;
+  const int qr0 = kb * kKvKeys;                    // first row touching these keys (128-aligned)
+  const int nstep_h = (p.T - qr0 + kKvRows - 1) / kKvRows;  // 128-row steps per head
+  const int n_it = hpt * nstep_h;
 
   Stager<D, kKvWaves> qs_stage, gs_stage;
   qs_stage.init(p.sq[2], wave, lane);
@@ -554,69 +707,44 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   const int rbase_op = TL::row_base(lane);
   const int tbase_op = TL::tr_base(lane);
 
-  auto stage = [&](int it, int buf) {
-    const int head = kvh * p.R + hs * hpt + it / nblk_q;
-    const int qb = qb0 + it % nblk_q;
-    qs_stage.stage(smem[buf][0], p.q + b * p.sq[0] + (int64_t)head * p.sq[1], p.sq[2], qb * kBlk, p.T);
-    gs_stage.stage(smem[buf][1], p.dout + b * p.sdo[0] + (int64_t)head * p.sdo[1], p.sdo[2], qb * kBlk, p.T);
+  // (head, first row) of a step, advanced without divisions
+  auto stage = [&](int head, int row0, int buf) {
+    const uint16_t* qh = p.q + b * p.sq[0] + (int64_t)head * p.sq[1];
+    const uint16_t* gh = p.dout + b * p.sdo[0] + (int64_t)head * p.sdo[1];
+    // both halves always (rows past T are clamped to row T-1, so the LDS
+    // never holds stale or uninitialised values that could reach a product)
+    qs_stage.stage(smem[buf][0], qh, p.sq[2], row0, p.T);
+    gs_stage.stage(smem[buf][1], gh, p.sdo[2], row0, p.T);
+    qs_stage.stage(smem[buf][0] + TL::BYTES, qh, p.sq[2], row0 + kBlk, p.T);
+    gs_stage.stage(smem[buf][1] + TL::BYTES, gh, p.sdo[2], row0 + kBlk, p.T);
     const int64_t rb = ((int64_t)b * p.Hq + head) * p.T;
-    if (wave == 0) stage_vec64(reinterpret_cast<char*>(vec[buf][0]), p.lse + rb, qb * kBlk, p.T, lane);
-    if (wave == 1) stage_vec64(reinterpret_cast<char*>(vec[buf][1]), p.delta + rb, qb * kBlk, p.T, lane);
+    const float* src = (wave & 2) ? p.delta + rb : p.lse2 + rb;
+    stage_vec64(reinterpret_cast<char*>(&vec[buf][wave >> 1][(wave & 1) * kBlk]), src, row0 + (wave & 1) * kBlk, p.T, lane);
   };
 
-  stage(0, 0);
+  int cur_row = qr0, nxt_head = kvh * p.R + hs * hpt, nxt_row = qr0;
+  stage(nxt_head, nxt_row, 0);
   wait_vmem();
   __syncthreads();
-
   const float c2 = p.scale_log2;
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
-    if (it + 1 < n_it) stage(it + 1, buf ^ 1);
-    const int qrow0 = (qb0 + it % nblk_q) * kBlk;
-    const char* Q = smem[buf][0];
-    const char* G = smem[buf][1];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      // skip a 32-row half whose rows all precede every key of this wave
-      if (!wave_live || k0 > qrow0 + mt * 32 + 31) continue;
-      f32x16 s, dp;
-      {
-        const V8 a = TL::template row_op<E>(Q, rbase_op, mt * 32, 0);
-        const V8 a2 = TL::template row_op<E>(G, rbase_op, mt * 32, 0);
-        s = E::mfma(a, kop[0], f32x16{});
-        dp = E::mfma(a2, vop[0], f32x16{});
-      }
-#pragma unroll
-      for (int kk = 1; kk < KT; ++kk) {
-        const V8 a = TL::template row_op<E>(Q, rbase_op, mt * 32, kk);
-        const V8 a2 = TL::template row_op<E>(G, rbase_op, mt * 32, kk);
-        s = E::mfma(a, kop[kk], s);
-        dp = E::mfma(a2, vop[kk], dp);
-      }
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int qr = mt * 32 + 8 * g4 + 4 * hh;   // first of 4 query rows in these slots
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&vec[buf][0][qr]);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&vec[buf][1][qr]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * g4 + e;
-          const int qg = qrow0 + qr + e;
-          float pv = exp2_fast(__builtin_fmaf(s[i], c2, -l4[e] * kLog2e));
-          if (key > qg || qg >= p.T) pv = 0.f;
-          s[i] = pv;
-          dp[i] = pv * (dp[i] - d4[e]);
-        }
-      }
-      const V8 p0 = pack8<E>(s, 0), p1 = pack8<E>(s, 8);
-      const V8 d0 = pack8<E>(dp, 0), d1 = pack8<E>(dp, 8);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        dvacc[dt] = E::mfma(TL::template tr_op<E>(G, tbase_op, 2 * mt, dt), p0, dvacc[dt]);
-        dkacc[dt] = E::mfma(TL::template tr_op<E>(Q, tbase_op, 2 * mt, dt), d0, dkacc[dt]);
-        dvacc[dt] = E::mfma(TL::template tr_op<E>(G, tbase_op, 2 * mt + 1, dt), p1, dvacc[dt]);
-        dkacc[dt] = E::mfma(TL::template tr_op<E>(Q, tbase_op, 2 * mt + 1, dt), d1, dkacc[dt]);
-      }
+    cur_row = nxt_row;
+    nxt_row += kKvRows;
+    if (nxt_row >= p.T) {
+      nxt_row = qr0;
+      ++nxt_head;
+    }
+    if (it + 1 < n_it) stage(nxt_head, nxt_row, buf ^ 1);
+    if (wave_live) {
+      // no mask when every key of the wave precedes every row and all rows are below T
+      const bool fast = (k0 + kKvKpw - 1 <= cur_row) && (cur_row + kKvRows <= p.T);
+      if (fast)
+        dkv_step<E, D, false>(smem[buf][0], smem[buf][1], vec[buf][0], vec[buf][1], kop, vop, dkacc, dvacc,
+                              rbase_op, tbase_op, lane, key, k0, cur_row, p.T, c2);
+      else
+        dkv_step<E, D, true>(smem[buf][0], smem[buf][1], vec[buf][0], vec[buf][1], kop, vop, dkacc, dvacc,
+                             rbase_op, tbase_op, lane, key, k0, cur_row, p.T, c2);
     }
     wait_vmem();
     __syncthreads();

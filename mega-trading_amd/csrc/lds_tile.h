@@ -1,11 +1,13 @@
 // LDS tiles of 64 rows x D 16-bit elements for the gfx950 attention kernels.
 //
 // Layout: rows are stored unpadded (RB = 2*D bytes); the 16-byte chunks of
-// row r are XOR-swizzled, chunk c living at slot c ^ (r % SW), so that the 8
-// lanes reading one chunk column of 8 consecutive rows hit 8 different slots.
-// Because the swizzle is an XOR with bits the operand offsets never touch,
-// every operand address is a per-lane base computed once, XOR-ed with a
-// per-step constant, plus an immediate row offset.
+// row r are XOR-swizzled, chunk c living at slot c ^ f(r).  For 8 chunks per
+// row and more, f(r) = 2*(r%4) + (r/4)%2: the 8 lanes of a ds_read_b128 phase
+// (one chunk column of 8 consecutive rows) hit 8 different slots, and the 16
+// lanes of a ds_read_b64_tr_b16 phase (4 consecutive rows x 2 neighbouring
+// chunks) hit 8 different slots too.  Because the swizzle is an XOR with bits
+// the operand offsets never touch, every operand address is a per-lane base
+// computed once, XOR-ed with a per-step constant, plus an immediate row offset.
 //
 // Staging uses global_load_lds_dwordx4: each lane of a wave copies 16 bytes
 // from its own global address straight into LDS at (wave base + 16 * lane),
@@ -42,12 +44,18 @@ struct Tile {
   static constexpr int BYTES = 64 * RB;         // one 64-row tile
   static constexpr int INSTR = NC;              // 1 KB wave instructions per tile (64 * NC * 16 B / 1 KB)
 
+  // slot permutation of row r (depends on r % 8 only)
+  static __device__ __forceinline__ int swz(int row) {
+    if constexpr (SW == 8) return ((row & 3) << 1) | ((row >> 2) & 1);
+    return row % SW;
+  }
+
   // --- operand addressing -------------------------------------------------
   // row_op base: lane (row = lane % 32, chunk = lane / 32) at r0 = 0, kk = 0.
   static __device__ __forceinline__ int row_base(int lane) {
     const int row = lane & 31;
     const int chunk = lane >> 5;
-    return row * RB + ((chunk ^ (row % SW)) << 4);
+    return row * RB + ((chunk ^ swz(row)) << 4);
   }
   // tr_op base: lane's 8-byte source at r0 = 0, c0 = 0 (first of the two reads).
   static __device__ __forceinline__ int tr_base(int lane) {
@@ -55,7 +63,7 @@ struct Tile {
     const int i = lane & 15;
     const int row = 4 * (g >> 1) + (i >> 2);
     const int col = 16 * (g & 1) + 4 * (i & 3);
-    return row * RB + (((col >> 3) ^ (row % SW)) << 4) + ((col & 7) << 1);
+    return row * RB + (((col >> 3) ^ swz(row)) << 4) + ((col & 7) << 1);
   }
 
   template <class E>
@@ -87,19 +95,25 @@ struct Stager {
   static_assert(TL::INSTR % NW == 0, "tile instructions must split evenly over the waves");
   static constexpr int N = TL::INSTR / NW;
   int off[N];   // row * row_stride + chunk * 8
-  int row[N];
-  int chunk[N];
   int lds_off;  // byte offset of this wave's first 1 KB block in the tile
+  int wave_, lane_;
+
+  static __device__ __forceinline__ void place(int i, int wave, int lane, int& row, int& chunk) {
+    const int f = (i * NW + wave) * 64 + lane;  // flat LDS chunk index
+    row = f / TL::NC;
+    chunk = (f % TL::NC) ^ TL::swz(row);
+  }
 
   __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int f = (i * NW + wave) * 64 + lane;  // flat LDS chunk index
-      row[i] = f / TL::NC;
-      chunk[i] = (f % TL::NC) ^ (row[i] % TL::SW);
-      off[i] = row[i] * (int)row_stride + chunk[i] * 8;
+      int row, chunk;
+      place(i, wave, lane, row, chunk);
+      off[i] = row * (int)row_stride + chunk * 8;
     }
     lds_off = wave * 1024;
+    wave_ = wave;
+    lane_ = lane;
   }
 
   // Stage rows [row0, row0 + 64) of the matrix at `src` (row stride as in init).
@@ -107,13 +121,14 @@ struct Stager {
     if (row0 + 64 <= T) {
       const uint16_t* tile = src + (int64_t)row0 * row_stride;
 #pragma unroll
-      for (int i = 0; i < N; ++i)
-        lds_dma16(tile + off[i], lds + lds_off + i * NW * 1024);
+      for (int i = 0; i < N; ++i) lds_dma16(tile + off[i], lds + lds_off + i * NW * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < N; ++i) {
-        const int grow = min(row0 + row[i], T - 1);
-        lds_dma16(src + (int64_t)grow * row_stride + chunk[i] * 8, lds + lds_off + i * NW * 1024);
+        int row, chunk;
+        place(i, wave_, lane_, row, chunk);
+        const int grow = min(row0 + row, T - 1);
+        lds_dma16(src + (int64_t)grow * row_stride + chunk * 8, lds + lds_off + i * NW * 1024);
       }
     }
   }
