@@ -151,11 +151,170 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t* x, int64
 // Forward
 // ===========================================================================
 // Lazy rescaling: the running row max m used as the exponent offset is only
-// raised when a tile's max exceeds it by more than kRescaleSlack (log2
-// units), so P = 2^(s*c - m) stays below 2^kRescaleSlack and most tiles skip
-// the O / l rescale.  O = acc / l and LSE = (m + log2 l) * ln 2 are exact for
-// any m, so the result does not depend on when rescales happen.
+// raised when a quarter's max exceeds it by more than kRescaleSlack (log2
+// units), so P = 2^(s*c - m) stays below 2^kRescaleSlack (fits fp16 too) and
+// most quarters skip the O / l rescale.  O = acc / l and LSE = (m + log2 l)
+// ln 2 are exact for any m, so the result does not depend on when rescales
+// happen.
 constexpr float kRescaleSlack = 8.0f;
+constexpr int kFwdKeys = 128;  // keys per staged K/V tile (two 64-row halves)
+
+// Multiply 8 packed 16-bit values by a scalar (rare path: rescaling a
+// quarter's P after the offset moved).
+template <class E>
+__device__ __forceinline__ typename E::v8 scale8(typename E::v8 x, float a) {
+  const u32x4 w = __builtin_bit_cast(u32x4, x);
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) r[p] = pack2<E>(lo_f<E>(w[p]) * a, hi_f<E>(w[p]) * a);
+  return __builtin_bit_cast(typename E::v8, r);
+}
+
+// One 128-key tile for one wave (64 query rows, two 32-row column tiles nt).
+// Quarter h = keys kt0 + 32h .. +31.  Pipeline (issue order):
+//   S0 | M0 | S1 + E0 | M1 | PV0 + S2 + E1 | M2 | PV1 + S3 + E2 | M3 | PV2 + E3 | PV3
+// Sh = scores of quarter h, Mh = its row max and (rare, wave-uniform)
+// rescale branch, Eh = its exponentials / row sums / packing, PVh = O += P V.
+// With MASK (the tile holding this wave's diagonal) keys above the query are
+// masked and quarters wholly above the wave's rows are skipped.
+template <class E, int D, bool MASK>
+__device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const typename E::v8 (*qop)[D / 16],
+                                         f32x16 (*oacc)[2], float* mrun, float* lrun, int rbase, int tbase,
+                                         int lane, int kt0, int q0, float c2) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+  const int hh = lane >> 5;
+  const int l32 = lane & 31;
+  bool live[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) live[h] = !MASK || (kt0 + 32 * h <= q0 + 63);
+
+  auto sq = [&](int h, f32x16* st) {
+    const char* Kh = K + (h >> 1) * TL::BYTES;
+    const int r0 = 32 * (h & 1);
+    V8 a = TL::template row_op<E>(Kh, rbase, r0, 0);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) st[nt] = E::mfma(a, qop[nt][0], f32x16{});
+#pragma unroll
+    for (int kk = 1; kk < KT; ++kk) {
+      a = TL::template row_op<E>(Kh, rbase, r0, kk);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) st[nt] = E::mfma(a, qop[nt][kk], st[nt]);
+    }
+  };
+  // row max + rescale decision; `prev` = the previous quarter's packed P
+  // (still to be multiplied into O), rescaled with O when the offset moves
+  auto mx = [&](int h, f32x16* st, V8 (*prev)[2], bool has_prev) {
+    if constexpr (MASK) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kr = kt0 + 32 * h + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if (kr > q0 + 32 * nt + l32) st[nt][i] = -INFINITY;
+        }
+    }
+    float m[2];
+    bool need = false;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v = fmaxf(v, st[nt][i]);
+      m[nt] = max_with_partner(v) * c2;
+      need |= m[nt] > mrun[nt] + kRescaleSlack;
+    }
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const float mnew = fmaxf(mrun[nt], m[nt]);
+        const float alpha = exp2_fast(mrun[nt] - mnew);
+        mrun[nt] = mnew;
+        lrun[nt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
+        if (has_prev) {
+          prev[nt][0] = scale8<E>(prev[nt][0], alpha);
+          prev[nt][1] = scale8<E>(prev[nt][1], alpha);
+        }
+      }
+    }
+  };
+  auto ex = [&](f32x16* st, V8 (*pk)[2]) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const float moff = mrun[nt];
+      float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = exp2_fast(__builtin_fmaf(st[nt][i], c2, -moff));
+        st[nt][i] = pv;
+        ls[i & 3] += pv;
+      }
+      lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+      pk[nt][0] = pack8<E>(st[nt], 0);
+      pk[nt][1] = pack8<E>(st[nt], 8);
+    }
+  };
+  auto pv = [&](int h, V8 (*pk)[2]) {
+    const char* Vh = Vt + (h >> 1) * TL::BYTES;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const V8 a = TL::template tr_op<E>(Vh, tbase, 2 * (h & 1) + k2, dt);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pk[nt][k2], oacc[dt][nt]);
+      }
+  };
+  constexpr int NS = 2 * KT;       // S MFMAs of a quarter
+  constexpr int NP = 4 * DT;       // PV MFMAs of a quarter
+
+  f32x16 st[2][2];                 // ring: two quarters' scores [slot][nt]
+  V8 pk[2][2][2];                  // ring: two quarters' packed P [slot][nt][k2]
+  if (live[0]) sq(0, st[0]);
+#pragma unroll
+  for (int i = 0; i < KT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    // M(h): needs S(h); may rescale the pending P(h-1)
+    if (live[h]) mx(h, st[h & 1], pk[(h + 1) & 1], h > 0 && live[h - 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    // region: PV(h-1) + S(h+1) MFMAs interleaved with E(h)
+    if (h > 0 && live[h - 1]) pv(h - 1, pk[(h + 1) & 1]);
+    if (h < 3 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
+    if (live[h]) ex(st[h & 1], pk[h & 1]);
+    constexpr int dummy = 0;
+    (void)dummy;
+    if (h > 0) {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      }
+    }
+    if (h < 3) {
+#pragma unroll
+      for (int i = 0; i < KT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (live[3]) pv(3, pk[1]);
+  (void)NS;
+}
 
 template <class E, int D, bool ROPE>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnParams p) {
@@ -163,7 +322,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   using TL = Tile<D>;
   constexpr int KT = D / 16;            // k-steps over d
   constexpr int DT = D / 32;            // 32-wide d tiles
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
+  // [buf][K, V] x 128 rows (two 64-row tiles back to back)
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];
 
   const RowTask task = row_task(p);
   const int tid = threadIdx.x;
@@ -175,8 +335,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   const int qb = task.sb * p.rb + wave / p.r_sub;   // this wave's row block
   const int q0 = qb * kBlk;
   const bool active = qb < p.nqb;
+  const int jw = (q0 + kBlk - 1) / kFwdKeys;        // this wave's diagonal tile
   // last KV tile any wave of the workgroup needs
-  const int jlast = min(p.nqb - 1, task.sb * p.rb + p.rb - 1);
+  const int last_row = min(p.T, (task.sb * p.rb + p.rb) * kBlk) - 1;
+  const int jlast = last_row / kFwdKeys;
 
   const uint16_t* kbase = p.k + task.b * p.sk[0] + (int64_t)task.kvh * p.sk[1];
   const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
@@ -220,91 +382,29 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   vs_stage.init(p.sv[2], wave, lane);
   const int rbase_op = TL::row_base(lane);
   const int tbase_op = TL::tr_base(lane);
+  auto stage = [&](int j, int buf) {
+    const int r0 = j * kFwdKeys;
+    ks_stage.stage(smem[buf][0], kbase, p.sk[2], r0, p.T);
+    vs_stage.stage(smem[buf][1], vbase, p.sv[2], r0, p.T);
+    ks_stage.stage(smem[buf][0] + TL::BYTES, kbase, p.sk[2], r0 + kBlk, p.T);
+    vs_stage.stage(smem[buf][1] + TL::BYTES, vbase, p.sv[2], r0 + kBlk, p.T);
+  };
 
-  ks_stage.stage(smem[0][0], kbase, p.sk[2], 0, p.T);
-  vs_stage.stage(smem[0][1], vbase, p.sv[2], 0, p.T);
+  stage(0, 0);
   wait_vmem();
   __syncthreads();
 
   const float c2 = p.scale_log2;
   for (int j = 0; j <= jlast; ++j) {
     const int buf = j & 1;
-    if (j < jlast) {
-      ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
-      vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
-    }
-    if (active && j <= qb) {
-      const char* K = smem[buf][0];
-      const char* Vt = smem[buf][1];
-      f32x16 st[2][2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        {
-          const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][0], f32x16{});
-        }
-#pragma unroll
-        for (int kk = 1; kk < KT; ++kk) {
-          const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, kk);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) st[mt][nt] = E::mfma(a, qop[nt][kk], st[mt][nt]);
-        }
-      }
-      // The two 32-key halves: the softmax of half 0 overlaps the S MFMAs of
-      // half 1, and half 0's PV MFMAs overlap the softmax of half 1.
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        if (j == qb) {
-          // diagonal tile: key (row m of S^T) > query (col n) is masked
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-              if (kr > nt * 32 + l32) st[mt][nt][i] = -INFINITY;
-            }
-        }
-        V8 pop[2][2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          float mx = -INFINITY;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[mt][nt][i]);
-          mx = max_with_partner(mx) * c2;
-          // wave-uniform: rescale only if some row's max outgrew its offset
-          if (__builtin_amdgcn_ballot_w64(mx > mrun[nt] + kRescaleSlack)) {
-            const float mnew = fmaxf(mrun[nt], mx);
-            const float alpha = exp2_fast(mrun[nt] - mnew);
-            mrun[nt] = mnew;
-            lrun[nt] *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
-          }
-          const float moff = mrun[nt];
-          float ls[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float pv = exp2_fast(__builtin_fmaf(st[mt][nt][i], c2, -moff));
-            st[mt][nt][i] = pv;
-            ls[i & 3] += pv;
-          }
-          lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-          pop[nt][0] = pack8<E>(st[mt][nt], 0);
-          pop[nt][1] = pack8<E>(st[mt][nt], 8);
-        }
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const V8 a = TL::template tr_op<E>(Vt, tbase_op, 2 * mt + k2, dt);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pop[nt][k2], oacc[dt][nt]);
-          }
-        }
-      }
+    if (j < jlast) stage(j + 1, buf ^ 1);
+    if (active && j <= jw) {
+      if (j < jw)
+        fwd_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                              j * kFwdKeys, q0, c2);
+      else
+        fwd_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                             j * kFwdKeys, q0, c2);
     }
     wait_vmem();
     __syncthreads();
