@@ -105,10 +105,10 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True):
 
 
 def time_kernels(pkg, cfg, iters):
-    """Average duration of each kernel stage, HIP events recorded on its launch stream.
-
-    The forward stage includes the 5 us K-RoPE pass and the dK/dV stage the
-    partial-sum combine pass that follows its kernel."""
+    """Average duration of each main kernel (HIP events the library records
+    around it on its launch stream, one pair per launch) and of each whole
+    stage: the forward stage adds the K-RoPE pass, the dK/dV stage the
+    partial-sum combine pass."""
     native = pkg._native
     lib = native.load()
     b, t, hq, hkv, d = cfg
@@ -143,20 +143,51 @@ def time_kernels(pkg, cfg, iters):
         for _, fn in stages:
             fn()
     torch.cuda.synchronize()
-    # each stage launched `iters` times back to back between two events on the
-    # launch stream, so per-launch event overhead does not inflate the average
     out = {}
     for name, fn in stages:
+        # the main kernel alone: a HIP event pair per launch, recorded by the
+        # library on the launch stream right around that kernel
+        pairs_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+        for a, b_ in pairs_ev:  # materialise the events on this device
+            a.record(stream)
+            b_.record(stream)
+        torch.cuda.synchronize()
+        for a, b_ in pairs_ev:
+            native.check(lib.mt_time_next_kernel(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b_.cuda_event)),
+                         "mt_time_next_kernel")
+            fn()
+        torch.cuda.synchronize()
+        ms = sum(a.elapsed_time(b_) for a, b_ in pairs_ev) / iters
+        # the whole stage (with its helper pass) launched `iters` times back to back
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(iters):
             fn()
         e1.record(stream)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / iters
+        stage_ms = e0.elapsed_time(e1) / iters
         flops = KERNEL_FLOP_UNITS[name] * b * hq * d * pairs(t)
-        out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flop": flops}
+        out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flop": flops,
+                     "stage_ms": stage_ms}
     return out
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_C3.txt")
+
+
+def hbm_traffic(kernel):
+    """HBM bytes per launch of `kernel` at C3 (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the copy-kernel calibration), from the committed rocprofv3
+    counter summary; None when the summary has no line for it."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        fields = dict(f.split("=", 1) for f in line.split() if "=" in f)
+        if fields.get("kernel") == kernel and "traffic_bytes" in fields:
+            return int(fields["traffic_bytes"])
+    return None
 
 
 def cpu_baseline(cfg):
@@ -262,9 +293,10 @@ def main(argv=None) -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": hbm_traffic(dom),
         },
-        "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1)} for n, x in kern.items()},
+        "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1), "stage_ms": round(x["stage_ms"], 4)}
+                    for n, x in kern.items()},
         "secondary": {
             "C2_fwd_bwd_tflops": round(fwd_bwd_flops(*C2[:1], C2[1], C2[2], C2[4]) / (ms_c2 * 1e-3) / 1e12, 2),
             "C2_ms_per_step": round(ms_c2, 4),

@@ -123,6 +123,19 @@ int mt_gqa_attn_bwd_dkv(const void* q, const void* k, const void* v, const void*
                         const int64_t* strides, float scale, int dtype,
                         const float* rope_cos, const float* rope_sin, void* stream);
 
+/*
+ * Kernel timing (no counterpart in the reference, whose benchmark times the
+ * whole op, scripts/benchmark_triton_attention.py:164-176).  Arms two created
+ * HIP events (hipEvent_t, passed as void*) that the next mt_gqa_attn_* call
+ * made by this thread attaches to its main kernel (attn_fwd, attn_bwd_dq or
+ * attn_bwd_dkv -- the first of these it launches) through hipExtLaunchKernel,
+ * so their elapsed time is that dispatch's own duration, without helper passes
+ * such as the K RoPE pass and the dK/dV partial-sum combine.  The events are
+ * disarmed after that launch.  Both NULL disarms.  For benchmarks and
+ * profilers.
+ */
+int mt_time_next_kernel(void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,7 @@ EXPORTS = (
     "mt_gqa_attn_bwd",
     "mt_gqa_attn_bwd_dq",
     "mt_gqa_attn_bwd_dkv",
+    "mt_time_next_kernel",
 )
 
 _lock = threading.Lock()
@@ -73,6 +74,8 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = _I
             fn.argtypes = _BWD_ARGTYPES
+        lib.mt_time_next_kernel.restype = _I
+        lib.mt_time_next_kernel.argtypes = [_P, _P]
         _lib = lib
         return lib
 

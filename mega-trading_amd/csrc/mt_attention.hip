@@ -4,6 +4,7 @@
 // The validation mirrors the reference's Python checks
 // (src/mega_trading/kernels/triton_attention.py:14-23) so a bad call fails
 // before any launch, with a message retrievable through mt_last_error().
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -29,6 +30,20 @@ int fail(int code, const char* fmt, ...) {
 int ok() {
   g_err[0] = '\0';
   return MT_OK;
+}
+
+// Events armed by mt_time_next_kernel(): attached to the next main kernel
+// launch made by this thread (hipExtLaunchKernel stamps them with that
+// dispatch's own start and end), then disarmed.
+thread_local hipEvent_t g_time_start = nullptr;
+thread_local hipEvent_t g_time_stop = nullptr;
+
+template <class K>
+hipError_t launch_main(K kernel, dim3 grid, dim3 block, hipStream_t st, const mt::AttnParams& p) {
+  hipEvent_t a = g_time_start, b = g_time_stop;
+  g_time_start = g_time_stop = nullptr;
+  hipExtLaunchKernelGGL(kernel, grid, block, 0, st, a, b, 0, p);
+  return hipGetLastError();
 }
 
 // One [B,H,T,D] tensor: d stride must be 1, rows 16-byte aligned.
@@ -134,8 +149,7 @@ hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
     p.sk[2] = D;
   }
   dim3 grid(p.nsb * p.B * p.Hkv * p.n_hsub);
-  hipLaunchKernelGGL((mt::attn_fwd_kernel<E, D, ROPE>), grid, dim3(256), 0, st, p);
-  return hipGetLastError();
+  return launch_main(mt::attn_fwd_kernel<E, D, ROPE>, grid, dim3(256), st, p);
 }
 
 // stage: 1 = dQ (+ delta), 2 = dK/dV, 3 = both
@@ -143,14 +157,12 @@ template <class E, int D, bool ROPE>
 hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
   if (stage & 1) {
     dim3 grid_dq(p.nsb * p.B * p.Hkv * p.n_hsub);
-    hipLaunchKernelGGL((mt::attn_bwd_dq_kernel<E, D, ROPE>), grid_dq, dim3(256), 0, st, p);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE>, grid_dq, dim3(256), st, p);
     if (e != hipSuccess) return e;
   }
   if (stage & 2) {
     dim3 grid_kv(p.nkb * p.B * p.Hkv * p.n_split);
-    hipLaunchKernelGGL((mt::attn_bwd_dkv_kernel<E, D, ROPE>), grid_kv, dim3(64 * mt::kKvWaves), 0, st, p);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_main(mt::attn_bwd_dkv_kernel<E, D, ROPE>, grid_kv, dim3(64 * mt::kKvWaves), st, p);
     if (e != hipSuccess) return e;
     if (p.n_split > 1) {
       const int64_t n4 = (int64_t)p.B * p.Hkv * p.T * (D / 4);
@@ -236,9 +248,17 @@ int bwd_impl(int stage, const void* q, const void* k, const void* v, const void*
 
 extern "C" {
 
-int mt_version(void) { return (0 << 16) | 2; }
+int mt_version(void) { return (0 << 16) | 3; }
 
 const char* mt_last_error(void) { return g_err; }
+
+int mt_time_next_kernel(void* start_event, void* stop_event) {
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(MT_E_NULL, "start_event and stop_event must both be given or both be NULL");
+  g_time_start = static_cast<hipEvent_t>(start_event);
+  g_time_stop = static_cast<hipEvent_t>(stop_event);
+  return ok();
+}
 
 size_t mt_gqa_attn_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D) {
   if (B < 1 || Hq < 1 || Hkv < 1 || T < 1 || Hq % Hkv) return 0;

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(mta):
     assert declared == sorted(mta._native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/mt_attention.h but not exported"
-    assert lib.mt_version() == (0 << 16) | 2
+    assert lib.mt_version() == (0 << 16) | 3
 
 
 def test_library_is_gfx950_only(mta):
@@ -46,6 +46,14 @@ def _fwd_call(lib, q=0x1000, k=0x1000, v=0x1000, o=0x1000, lse=0x1000, b=1, hq=4
         strides = [hq * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hq * t * d, t * d, d, 1]
     arr = (ctypes.c_int64 * 16)(*strides)
     return lib.mt_gqa_attn_fwd(q, k, v, o, lse, qrot, krot, b, hq, hkv, t, d, arr, 0.125, dtype, cos, sin, None)
+
+
+def test_kernel_timer_arming(mta):
+    lib = mta._native.load()
+    assert lib.mt_time_next_kernel(0x1000, None) == -1
+    assert b"both" in lib.mt_last_error()
+    assert lib.mt_time_next_kernel(None, None) == 0  # disarm
+    assert lib.mt_last_error() == b""
 
 
 def test_c_abi_rejects_bad_arguments_before_launch(mta):
