@@ -248,12 +248,12 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const float moff = mrun[nt];
-      float ls[4] = {0.f, 0.f, 0.f, 0.f};
+      float ls[4];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float pv = exp2_fast(__builtin_fmaf(st[nt][i], c2, -moff));
         st[nt][i] = pv;
-        ls[i & 3] += pv;
+        ls[i & 3] = i < 4 ? pv : ls[i & 3] + pv;
       }
       lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
       pk[nt][0] = pack8<E>(st[nt], 0);
@@ -276,7 +276,9 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
 
   f32x16 st[2][2];                 // ring: two quarters' scores [slot][nt]
   V8 pk[2][2][2];                  // ring: two quarters' packed P [slot][nt][k2]
+  // LDS operand reads run one step ahead of the MFMAs that consume them
   if (live[0]) sq(0, st[0]);
+  __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
   for (int i = 0; i < KT; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -295,12 +297,15 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
     constexpr int dummy = 0;
     (void)dummy;
     if (h > 0) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-      for (int i = 0; i < NP; ++i) {
+      for (int i = 0; i < NP / 2; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
       }
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     if (h < 3) {
 #pragma unroll

@@ -82,12 +82,29 @@ struct Tile {
   }
 };
 
+// Global -> LDS copies (global_load_lds_dword[x4]: M0 = the wave's LDS base,
+// lane L's bytes land at M0 + size * L).  Issued from inline assembly so the
+// compiler does not track them: it would otherwise make the first
+// ds_read_b64_tr_b16 after each copy wait for every outstanding copy (it cannot
+// tell that the copy targets the other buffer), serialising the next tile's
+// prefetch with the current tile's compute.  Completion is enforced explicitly:
+// every copied buffer is read only after wait_vmem() and a workgroup barrier,
+// and a buffer is refilled only after the barrier that ends its last reads.
+__device__ __forceinline__ uint32_t lds_addr(const void* l) {
+  return (uint32_t)(uintptr_t)l;
+}
+
+__device__ __forceinline__ void lds_dma16(const uint16_t* g, char* l) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
+}
+
+__device__ __forceinline__ void lds_dma4(const float* g, char* l) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
+}
+
 // Staging of one 64-row tile by the NW waves of a workgroup: per-lane source
 // offsets (elements, relative to the tile's first row) of the INSTR/NW wave
 // instructions this wave issues, computed once.
-__device__ __forceinline__ void lds_dma16(const uint16_t* g, char* l) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)l, 16, 0, 0);
-}
 
 template <int D, int NW>
 struct Stager {
@@ -136,8 +153,7 @@ struct Stager {
 
 // Stage 64 fp32 values (row-indexed vector, clamped at T-1) with one wave.
 __device__ __forceinline__ void stage_vec64(char* lds, const float* src, int row0, int T, int lane) {
-  const float* g = src + min(row0 + lane, T - 1);
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+  lds_dma4(src + min(row0 + lane, T - 1), lds);
 }
 
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
