@@ -9,11 +9,16 @@
   14 * B * Hq * D * T(T+1)/2 (scripts/benchmark_triton_attention.py:179-190
   gives the forward 4 * B * Hq * D * T(T+1)/2; backward adds 2.5x).
 * roofline: the dominant kernel's algorithmic MFMA FLOPs per launch over its
-  average duration, timed live with HIP events on the launch stream.
+  average duration, from HIP events that the library attaches to that
+  kernel's own dispatches (mt_time_next_kernel) on the launch stream; traffic
+  is its HBM bytes per launch from the committed rocprofv3 counter summary.
 * cpu_baseline: the reference's CPU attention path (torch SDPA, fp32, forward
   + autograd backward, model.py:228-235) on the host cores over a bounded
   sample of the same workload.
-* secondary: BASELINE config 2 (T=1024) fwd+bwd TFLOP/s and the un-fused op.
+* secondary: BASELINE config 2 (T=1024) fwd+bwd TFLOP/s, the un-fused op, and
+  train tokens/sec of the 8-layer decoder with the HIP
+  attention in every layer against the same model on the reference's SDPA
+  route (the "train tokens/sec" half of the metric).
 """
 
 from __future__ import annotations
@@ -227,12 +232,53 @@ def cpu_baseline(cfg):
     }
 
 
+def sdpa_backends_usable(d=64, repeats=4):
+    """Which forced SDPA backends accept a causal GQA bf16 call of head dim d on this GPU."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    import torch.nn.functional as F
+
+    q = torch.randn(1, 2 * repeats, 128, d, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 128, d, device="cuda", dtype=torch.bfloat16)
+    ok = []
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION), ("efficient", SDPBackend.EFFICIENT_ATTENTION),
+                     ("math", SDPBackend.MATH)):
+        try:
+            with sdpa_kernel(be):
+                F.scaled_dot_product_attention(q, k, k, is_causal=True, enable_gqa=True)
+            ok.append(name)
+        except RuntimeError:
+            pass
+    torch.cuda.synchronize()
+    return ok
+
+
+def train_tokens_per_second(pkg, steps, warmup):
+    """8-layer decoder train step, HIP attention route vs the
+    reference's SDPA route, same seeded weights and Zipf batch."""
+    wl = pkg.workload
+    ids, labels = wl.zipf_batch(wl.C5_BATCH, wl.C5_SEQ, wl.C5_MODEL["vocab_size"])
+    out = {}
+    for name, backend in (("hip", "hip"), ("sdpa", "auto")):
+        model = wl.build_model(backend, seed=0, device="cuda")
+        step = wl.TrainStep(model, ids, labels)
+        tps, ms, loss = step.tokens_per_second(steps, warmup)
+        out[name] = {"tokens_per_s": round(tps, 1), "ms_per_step": round(ms, 3), "loss": round(loss, 4)}
+        del step, model
+        torch.cuda.empty_cache()
+    out["speedup"] = round(out["hip"]["tokens_per_s"] / out["sdpa"]["tokens_per_s"], 4)
+    out["sdpa_backends_usable"] = sdpa_backends_usable()
+    out["workload"] = ("8-layer decoder d_model 512, Hq 8 Hkv 2 D 64, SwiGLU 1408, vocab 16384, B=32 T=1024 Zipf(1.1) "
+                       f"tokens, bf16 autocast + fused AdamW; {steps} timed steps after {warmup} warm-up")
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-train", action="store_true", help="skip the config 5 train-step tokens/sec leg")
     ap.add_argument("--kernels-only", action="store_true",
                     help="profiling driver: run only the C3 kernels stage by stage, then a 256 MiB device copy "
                          "(the reference kernel for HBM-traffic counter calibration), and print their timings")
@@ -304,6 +350,8 @@ def main(argv=None) -> int:
             "wall_ms_per_step": round(ms_wall, 4),
         },
     }
+    if not args.no_train:
+        line["secondary"]["C5_train"] = train_tokens_per_second(pkg, steps=20, warmup=5)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(C3)
     print(json.dumps(line), flush=True)

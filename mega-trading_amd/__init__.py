@@ -9,9 +9,11 @@ name carries a hyphen).  Public API:
   the interleaved RoPE of ``model.py:223`` fused into the kernels.
 * ``attention_forward(...)`` -- forward returning ``(output, logsumexp)``.
 * ``model`` -- the Llama-style order-flow decoder that calls them
-  (``attention_backend="hip"``).
+  (``attention_backend="triton"`` or ``"hip"``), and ``workload`` -- its
+  8-layer train step on synthetic Zipf tokens (the tokens/sec benchmark).
 """
 
+from . import model, workload
 from .attention import SUPPORTED_HEAD_DIMS, attention, attention_forward, rope_attention
 
-__all__ = ["attention", "rope_attention", "attention_forward", "SUPPORTED_HEAD_DIMS"]
+__all__ = ["attention", "rope_attention", "attention_forward", "SUPPORTED_HEAD_DIMS", "model", "workload"]

@@ -1,0 +1,279 @@
+"""Llama-style decoder restated around the HIP attention op.
+
+The module tree, argument names and routing follow the reference model
+(``src/mega_trading/model.py:20-131`` TradingModel, ``:150-187`` decoder block,
+``:189-237`` LlamaAttention, ``:240-269`` SwiGLU / RMSNorm, ``:272-316`` RoPE,
+``:319-330`` init), so the train step the reference measures in tokens/sec
+(``trainer.py:333-346``) can run on MI355X with either attention path:
+
+* ``attention_backend`` in {"auto", "flash", "efficient", "math"}: RoPE in
+  torch (tables cast to the activation dtype, ``model.py:290-291``) then
+  ``F.scaled_dot_product_attention(is_causal=True, enable_gqa=...)``
+  (``model.py:228-235``) -- the reference's eager path;
+* ``"triton"`` (the reference's value, kept so its configs work unchanged) or
+  ``"hip"`` with ``dropout_p == 0`` (``model.py:225``): the gfx950 kernels.  By
+  default RoPE is fused into them (``rope_attention`` with the fp32 tables);
+  ``fuse_rope=False`` keeps the reference's two calls, ``self.rope`` then
+  ``attention(query, key, value, repeats=...)`` (``model.py:223,226``).
+
+Only the attention is a HIP kernel here; RMSNorm, SwiGLU and the loss use
+torch ops (the reference's Triton versions of those are separate operators).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .attention import attention as _hip_attention
+from .attention import rope_attention as _hip_rope_attention
+
+__all__ = ["TradingModel", "LlamaDecoderBlock", "LlamaAttention", "SwiGLU", "RMSNorm", "RotaryEmbedding",
+           "ATTENTION_BACKENDS", "HIP_BACKENDS"]
+
+ATTENTION_BACKENDS = ("auto", "flash", "efficient", "math", "triton", "hip")
+HIP_BACKENDS = ("triton", "hip")
+
+
+class TradingModel(nn.Module):
+    """Causal decoder with tied embeddings and next-token cross entropy (``model.py:20-131``)."""
+
+    def __init__(
+        self,
+        vocab_size: int,
+        block_size: int,
+        hidden_dim: int = 128,
+        layers: int = 4,
+        attention_heads: int = 4,
+        kv_heads: int | None = None,
+        intermediate_dim: int | None = None,
+        dropout: float = 0.1,
+        rope_theta: float = 500_000.0,
+        norm_eps: float = 1e-5,
+        attention_backend: str = "auto",
+        fuse_rope: bool = True,
+    ) -> None:
+        super().__init__()
+        if hidden_dim % attention_heads != 0:
+            raise ValueError("hidden_dim must be divisible by attention_heads")
+        kv_heads = kv_heads or attention_heads
+        if attention_heads % kv_heads != 0:
+            raise ValueError("attention_heads must be divisible by kv_heads")
+        self.vocab_size = vocab_size
+        self.block_size = block_size
+        self.hidden_dim = hidden_dim
+        self.attention_heads = attention_heads
+        self.kv_heads = kv_heads
+        self.operator_backend = attention_backend
+        self.token_embedding = nn.Embedding(vocab_size, hidden_dim)
+        self.blocks = nn.ModuleList(
+            [
+                LlamaDecoderBlock(
+                    hidden_dim=hidden_dim,
+                    block_size=block_size,
+                    attention_heads=attention_heads,
+                    kv_heads=kv_heads,
+                    intermediate_dim=intermediate_dim,
+                    dropout=dropout,
+                    rope_theta=rope_theta,
+                    norm_eps=norm_eps,
+                    attention_backend=attention_backend,
+                    fuse_rope=fuse_rope,
+                )
+                for _ in range(layers)
+            ]
+        )
+        self.norm = RMSNorm(hidden_dim, eps=norm_eps)
+        self.output = nn.Linear(hidden_dim, vocab_size, bias=False)
+        self.apply(_init_weights)
+        self.output.weight = self.token_embedding.weight  # tied after init, as model.py:71
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return self.output(self._hidden(input_ids))
+
+    def forward_with_loss(
+        self,
+        input_ids: torch.Tensor,
+        labels: torch.Tensor,
+        *,
+        return_logits: bool,
+        ignore_index: int = -100,
+    ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """Network plus next-token cross entropy (``model.py:84-131``, torch loss head)."""
+        if labels.shape != input_ids.shape:
+            raise ValueError("labels must match input_ids shape")
+        logits = self.output(self._hidden(input_ids))
+        loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), labels.reshape(-1), ignore_index=ignore_index)
+        return loss, (logits if return_logits else None)
+
+    def _hidden(self, input_ids: torch.Tensor) -> torch.Tensor:
+        if input_ids.ndim != 2:
+            raise ValueError("input_ids must have shape [batch, time]")
+        if input_ids.shape[1] > self.block_size:
+            raise ValueError(f"sequence length {input_ids.shape[1]} exceeds block_size {self.block_size}")
+        hidden = self.token_embedding(input_ids)
+        for block in self.blocks:
+            hidden = block(hidden)
+        return self.norm(hidden)
+
+
+class LlamaDecoderBlock(nn.Module):
+    """Pre-norm block: x + attn(norm(x)), then + ffn(norm(x)) (``model.py:150-187``)."""
+
+    def __init__(
+        self,
+        hidden_dim: int,
+        block_size: int,
+        attention_heads: int,
+        kv_heads: int,
+        intermediate_dim: int | None,
+        dropout: float,
+        rope_theta: float,
+        norm_eps: float,
+        attention_backend: str,
+        fuse_rope: bool = True,
+    ) -> None:
+        super().__init__()
+        self.attention_norm = RMSNorm(hidden_dim, eps=norm_eps)
+        self.attention = LlamaAttention(
+            hidden_dim=hidden_dim,
+            block_size=block_size,
+            attention_heads=attention_heads,
+            kv_heads=kv_heads,
+            dropout=dropout,
+            rope_theta=rope_theta,
+            attention_backend=attention_backend,
+            fuse_rope=fuse_rope,
+        )
+        self.ffn_norm = RMSNorm(hidden_dim, eps=norm_eps)
+        self.feed_forward = SwiGLU(hidden_dim, intermediate_dim or _llama_intermediate_dim(hidden_dim), dropout)
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        hidden = hidden + self.attention(self.attention_norm(hidden))
+        return hidden + self.feed_forward(self.ffn_norm(hidden))
+
+
+class LlamaAttention(nn.Module):
+    """Causal GQA self-attention with RoPE (``model.py:189-237``)."""
+
+    def __init__(
+        self,
+        hidden_dim: int,
+        block_size: int,
+        attention_heads: int,
+        kv_heads: int,
+        dropout: float,
+        rope_theta: float,
+        attention_backend: str = "auto",
+        fuse_rope: bool = True,
+    ) -> None:
+        super().__init__()
+        if attention_backend not in ATTENTION_BACKENDS:
+            raise ValueError("attention_backend must be one of: " + ", ".join(ATTENTION_BACKENDS))
+        self.attention_heads = attention_heads
+        self.kv_heads = kv_heads
+        self.head_dim = hidden_dim // attention_heads
+        self.repeats = attention_heads // kv_heads
+        self.q_proj = nn.Linear(hidden_dim, attention_heads * self.head_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_dim, kv_heads * self.head_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_dim, kv_heads * self.head_dim, bias=False)
+        self.o_proj = nn.Linear(hidden_dim, hidden_dim, bias=False)
+        self.rope = RotaryEmbedding(self.head_dim, block_size, theta=rope_theta)
+        self.dropout = dropout
+        self.rope_theta = rope_theta
+        self.attention_backend = attention_backend
+        self.fuse_rope = fuse_rope
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        batch_size, sequence_length, hidden_dim = hidden.shape
+        # [B, T, H*D] -> [B, H, T, D] strided views, as model.py:220-222
+        query = self.q_proj(hidden).view(batch_size, sequence_length, self.attention_heads, self.head_dim).transpose(1, 2)
+        key = self.k_proj(hidden).view(batch_size, sequence_length, self.kv_heads, self.head_dim).transpose(1, 2)
+        value = self.v_proj(hidden).view(batch_size, sequence_length, self.kv_heads, self.head_dim).transpose(1, 2)
+        dropout_p = self.dropout if self.training else 0.0
+        if self.attention_backend in HIP_BACKENDS and dropout_p == 0.0:
+            if self.fuse_rope:
+                attended = _hip_rope_attention(query, key, value, self.rope.cos, self.rope.sin, repeats=self.repeats)
+            else:
+                query, key = self.rope(query, key)
+                attended = _hip_attention(query, key, value, repeats=self.repeats)
+        else:
+            query, key = self.rope(query, key)
+            attended = F.scaled_dot_product_attention(
+                query, key, value, dropout_p=dropout_p, is_causal=True, enable_gqa=self.repeats > 1
+            )
+        attended = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, hidden_dim)
+        return self.o_proj(attended)
+
+
+class SwiGLU(nn.Module):
+    """w2(silu(w1 x) * w3 x) (``model.py:240-256``)."""
+
+    def __init__(self, hidden_dim: int, intermediate_dim: int, dropout: float) -> None:
+        super().__init__()
+        self.w1 = nn.Linear(hidden_dim, intermediate_dim, bias=False)
+        self.w2 = nn.Linear(intermediate_dim, hidden_dim, bias=False)
+        self.w3 = nn.Linear(hidden_dim, intermediate_dim, bias=False)
+        self.dropout = nn.Dropout(dropout)
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        return self.w2(self.dropout(F.silu(self.w1(hidden)) * self.w3(hidden)))
+
+
+class RMSNorm(nn.Module):
+    """``F.rms_norm`` with a learned scale (``model.py:259-269``)."""
+
+    def __init__(self, hidden_dim: int, eps: float = 1e-5) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_dim))
+        self.eps = eps
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(hidden, (hidden.shape[-1],), self.weight, eps=self.eps)
+
+
+class RotaryEmbedding(nn.Module):
+    """fp32 tables cos/sin [1, 1, T_max, D/2] of pos * theta^(-2i/D) (``model.py:272-294``)."""
+
+    def __init__(self, head_dim: int, max_sequence_length: int, theta: float) -> None:
+        super().__init__()
+        if head_dim % 2 != 0:
+            raise ValueError("RoPE requires an even head dimension")
+        positions = torch.arange(max_sequence_length, dtype=torch.float32)
+        inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+        freqs = torch.outer(positions, inv_freq)
+        self.register_buffer("cos", freqs.cos().view(1, 1, max_sequence_length, head_dim // 2), persistent=False)
+        self.register_buffer("sin", freqs.sin().view(1, 1, max_sequence_length, head_dim // 2), persistent=False)
+
+    def forward(self, query: torch.Tensor, key: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        sequence_length = query.shape[-2]
+        if sequence_length > self.cos.shape[-2]:
+            raise ValueError(f"sequence length {sequence_length} exceeds RoPE cache length {self.cos.shape[-2]}")
+        cos = self.cos[:, :, :sequence_length].to(dtype=query.dtype)
+        sin = self.sin[:, :, :sequence_length].to(dtype=query.dtype)
+        return rotate(query, cos, sin), rotate(key, cos, sin)
+
+
+def rotate(value: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Interleaved-pair rotation (x0, x1) -> (x0 c - x1 s, x0 s + x1 c) (``model.py:312-316``)."""
+    even = value[..., 0::2]
+    odd = value[..., 1::2]
+    return torch.stack((even * cos - odd * sin, even * sin + odd * cos), dim=-1).flatten(start_dim=-2)
+
+
+def _init_weights(module: nn.Module) -> None:
+    """N(0, 0.02) weights, zero biases (``model.py:319-326``)."""
+    if isinstance(module, nn.Linear):
+        nn.init.normal_(module.weight, mean=0.0, std=0.02)
+        if module.bias is not None:
+            nn.init.zeros_(module.bias)
+    elif isinstance(module, nn.Embedding):
+        nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+
+def _llama_intermediate_dim(hidden_dim: int) -> int:
+    """8/3 d_model rounded up to a multiple of 16 (``model.py:329-331``)."""
+    return int(math.ceil((8 * hidden_dim / 3) / 16) * 16)

@@ -1,0 +1,94 @@
+"""The 8-layer decoder train step and its synthetic data.
+
+Model shape: d_model 512, 8 query / 2 key-value heads of 64, SwiGLU 1408,
+8 layers, vocabulary 16384 with tied embeddings, N(0, 0.02) init, RoPE theta
+500 000 (the reference configs' value, ``configs/default.yaml:37``), dropout 0
+so the attention routes to the HIP kernels (``model.py:225``).  Batch: 32
+sequences of 1024 token ids drawn i.i.d. from a Zipf(1.1) law over the
+vocabulary ranks, split into inputs and next-token labels as
+``dataset.py:134-140`` (``tokens_to_example``) does.
+
+A step is what ``trainer.py:333-346`` times: bf16 autocast forward, cross
+entropy, backward, fused AdamW step and ``zero_grad``; tokens/sec counts the
+label tokens of the timed steps over their wall time, synchronised at both
+ends (``trainer.py:686-702``).
+"""
+
+from __future__ import annotations
+
+import time
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .model import TradingModel
+
+__all__ = ["C5_MODEL", "C5_BATCH", "C5_SEQ", "zipf_batch", "build_model", "TrainStep"]
+
+C5_MODEL = dict(
+    vocab_size=16384,
+    block_size=1024,
+    hidden_dim=512,
+    layers=8,
+    attention_heads=8,
+    kv_heads=2,
+    intermediate_dim=1408,
+    dropout=0.0,
+    rope_theta=500_000.0,
+)
+C5_BATCH = 32
+C5_SEQ = 1024
+
+
+def zipf_batch(batch: int, seq_len: int, vocab: int, *, exponent: float = 1.1, seed: int = 0):
+    """(input_ids, labels) int64 [batch, seq_len]: token ids with P(rank k) ~ k^-exponent,
+    k = 1..vocab (id = k - 1), drawn with numpy PCG64(seed) as one [batch, seq_len + 1] block."""
+    ranks = np.arange(1, vocab + 1, dtype=np.float64)
+    p = ranks ** -exponent
+    p /= p.sum()
+    rng = np.random.Generator(np.random.PCG64(seed))
+    ids = torch.from_numpy(rng.choice(vocab, size=(batch, seq_len + 1), p=p).astype(np.int64))
+    return ids[:, :-1].contiguous(), ids[:, 1:].contiguous()
+
+
+def build_model(attention_backend: str, *, seed: int = 0, device="cuda", **overrides) -> TradingModel:
+    """C5 model (or a variant via ``overrides``) with seeded N(0, 0.02) weights, fp32 master copy."""
+    cfg = dict(C5_MODEL)
+    cfg.update(overrides)
+    torch.manual_seed(seed)
+    return TradingModel(attention_backend=attention_backend, **cfg).to(device)
+
+
+class TrainStep:
+    """One optimisation step of ``model`` on a fixed batch (bf16 autocast, fused AdamW)."""
+
+    def __init__(self, model: TradingModel, input_ids: torch.Tensor, labels: torch.Tensor, *, lr: float = 3e-4):
+        self.model = model
+        dev = next(model.parameters()).device
+        self.input_ids = input_ids.to(dev)
+        self.labels = labels.to(dev)
+        self.optimizer = torch.optim.AdamW(model.parameters(), lr=lr, fused=dev.type == "cuda")
+        self.device = dev
+
+    def __call__(self) -> torch.Tensor:
+        self.model.train()
+        with torch.autocast(device_type=self.device.type, dtype=torch.bfloat16):
+            logits = self.model(self.input_ids)
+            loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), self.labels.reshape(-1))
+        loss.backward()
+        self.optimizer.step()
+        self.optimizer.zero_grad(set_to_none=True)
+        return loss.detach()
+
+    def tokens_per_second(self, steps: int, warmup: int) -> tuple[float, float, float]:
+        """(tokens/s, ms/step, last loss) over ``steps`` timed steps after ``warmup``."""
+        for _ in range(warmup):
+            self()
+        torch.cuda.synchronize(self.device)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = self()
+        torch.cuda.synchronize(self.device)
+        elapsed = time.perf_counter() - t0
+        return self.labels.numel() * steps / elapsed, elapsed / steps * 1e3, float(loss)

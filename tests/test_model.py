@@ -1,0 +1,149 @@
+"""CPU tests of the restated decoder: attention routing (as the reference's
+tests/test_training.py:421-461 checks it), RoPE tables, init, the C5 shape and
+its synthetic data."""
+
+from __future__ import annotations
+
+import importlib
+import math
+from unittest.mock import patch
+
+import numpy as np
+import pytest
+import torch
+
+model_mod = importlib.import_module("mega-trading_amd.model")
+workload = importlib.import_module("mega-trading_amd.workload")
+
+
+def _attn(backend="auto", **kw):
+    args = dict(hidden_dim=16, block_size=8, attention_heads=4, kv_heads=2, dropout=0.0, rope_theta=10_000.0)
+    args.update(kw)
+    return model_mod.LlamaAttention(attention_backend=backend, **args)
+
+
+def test_backend_values_validated():
+    with pytest.raises(ValueError, match="attention_backend must be one of"):
+        _attn("cuda")
+    for b in ("auto", "flash", "efficient", "math", "triton", "hip"):
+        _attn(b)
+
+
+def test_sdpa_route_uses_native_gqa():
+    attention = _attn("auto")
+    hidden = torch.randn(1, 8, 16)
+    with patch("mega-trading_amd.model.F.scaled_dot_product_attention", return_value=torch.zeros(1, 4, 8, 4)) as sdpa:
+        attention(hidden)
+    _q, key, value = sdpa.call_args.args[:3]
+    assert key.shape[1] == 2 and value.shape[1] == 2
+    assert sdpa.call_args.kwargs["enable_gqa"] is True
+    assert sdpa.call_args.kwargs["is_causal"] is True
+
+
+@pytest.mark.parametrize("backend", ["triton", "hip"])
+def test_hip_backend_calls_local_kernel(backend):
+    attention = _attn(backend, fuse_rope=False)
+    hidden = torch.randn(1, 8, 16)
+    with patch("mega-trading_amd.model._hip_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
+        out = attention(hidden)
+    query, key, value = op.call_args.args[:3]
+    assert out.shape == hidden.shape
+    assert query.shape == (1, 4, 8, 4) and key.shape[1] == 2 and value.shape[1] == 2
+    assert op.call_args.kwargs["repeats"] == 2
+    # RoPE was applied in torch before the call, as model.py:223 does
+    raw_q = attention.q_proj(hidden).view(1, 8, 4, 4).transpose(1, 2)
+    assert torch.allclose(query, attention.rope(raw_q, raw_q)[0])
+
+
+def test_fused_rope_route_passes_fp32_tables_and_raw_qk():
+    attention = _attn("hip")
+    hidden = torch.randn(1, 8, 16)
+    with patch("mega-trading_amd.model._hip_rope_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
+        attention(hidden)
+    query, key, value, cos, sin = op.call_args.args[:5]
+    assert op.call_args.kwargs["repeats"] == 2
+    assert cos is attention.rope.cos and sin is attention.rope.sin and cos.dtype == torch.float32
+    raw_q = attention.q_proj(hidden).view(1, 8, 4, 4).transpose(1, 2)
+    assert torch.equal(query, raw_q)  # un-rotated: the kernel rotates on load
+    assert query.stride() == raw_q.stride()  # the strided view is passed as is
+
+
+def test_dropout_in_training_falls_back_to_sdpa():
+    attention = _attn("hip", dropout=0.1)
+    attention.train()
+    hidden = torch.randn(1, 8, 16)
+    with patch("mega-trading_amd.model.F.scaled_dot_product_attention", return_value=torch.zeros(1, 4, 8, 4)) as sdpa, \
+            patch("mega-trading_amd.model._hip_rope_attention") as op:
+        attention(hidden)
+    assert sdpa.call_args.kwargs["dropout_p"] == 0.1
+    op.assert_not_called()
+    attention.eval()
+    with patch("mega-trading_amd.model._hip_rope_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
+        attention(hidden)
+    op.assert_called_once()
+
+
+def test_rope_tables_and_rotation_closed_form():
+    rope = model_mod.RotaryEmbedding(8, 16, theta=10_000.0)
+    assert rope.cos.shape == (1, 1, 16, 4)
+    pos, i = 5, 3
+    ang = pos * 10_000.0 ** (-2 * i / 8)
+    assert math.isclose(rope.cos[0, 0, pos, i].item(), math.cos(ang), rel_tol=1e-5, abs_tol=1e-6)
+    x = torch.randn(1, 2, 16, 8)
+    rq, rk = rope(x, x)
+    assert torch.allclose(rq[..., 0, :], x[..., 0, :])  # position 0 is the identity
+    assert torch.allclose(rq.norm(dim=-1), x.norm(dim=-1), atol=1e-5)  # rotations keep the norm
+    c, s = rope.cos[0, 0, pos, i], rope.sin[0, 0, pos, i]
+    x0, x1 = x[0, 0, pos, 2 * i], x[0, 0, pos, 2 * i + 1]
+    assert torch.allclose(rq[0, 0, pos, 2 * i], x0 * c - x1 * s, atol=1e-6)
+    assert torch.allclose(rq[0, 0, pos, 2 * i + 1], x0 * s + x1 * c, atol=1e-6)
+    with pytest.raises(ValueError, match="exceeds RoPE cache length"):
+        rope(torch.randn(1, 1, 17, 8), torch.randn(1, 1, 17, 8))
+
+
+def test_model_init_tying_and_c5_parameter_count():
+    m = model_mod.TradingModel(attention_backend="auto", **workload.C5_MODEL)
+    assert m.output.weight is m.token_embedding.weight
+    emb = m.token_embedding.weight.numel()
+    total = sum(p.numel() for p in m.parameters())
+    assert emb == 16384 * 512
+    # per layer: q, o 512x512; k, v 512x128; SwiGLU 3 x 512x1408; two norms of 512
+    per_layer = 2 * 512 * 512 + 2 * 512 * 128 + 3 * 512 * 1408 + 2 * 512
+    assert total == emb + 8 * per_layer + 512
+    w = m.blocks[0].attention.q_proj.weight
+    assert abs(w.std().item() - 0.02) < 1e-3
+    assert model_mod._llama_intermediate_dim(512) == 1376
+
+
+def test_model_forward_shapes_and_errors():
+    m = model_mod.TradingModel(vocab_size=32, block_size=8, hidden_dim=16, layers=2, attention_heads=4, kv_heads=2,
+                               dropout=0.0, rope_theta=10_000.0)
+    ids = torch.randint(0, 32, (2, 8))
+    assert m(ids).shape == (2, 8, 32)
+    loss, logits = m.forward_with_loss(ids, ids, return_logits=True)
+    assert logits.shape == (2, 8, 32) and loss.ndim == 0
+    assert abs(loss.item() - math.log(32)) < 0.5
+    with pytest.raises(ValueError, match="block_size"):
+        m(torch.randint(0, 32, (1, 9)))
+    with pytest.raises(ValueError, match="batch, time"):
+        m(torch.randint(0, 32, (8,)))
+
+
+def test_hip_route_on_cpu_tensors_raises():
+    m = model_mod.TradingModel(vocab_size=32, block_size=8, hidden_dim=256, layers=1, attention_heads=4, kv_heads=2,
+                               dropout=0.0, rope_theta=10_000.0, attention_backend="hip")
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        m(torch.randint(0, 32, (1, 8)))
+
+
+def test_zipf_batch_is_seeded_shifted_and_heavy_headed():
+    x, y = workload.zipf_batch(4, 256, 16384)
+    x2, y2 = workload.zipf_batch(4, 256, 16384)
+    assert torch.equal(x, x2) and torch.equal(y, y2)
+    assert x.shape == y.shape == (4, 256) and x.dtype == torch.int64
+    assert torch.equal(x[:, 1:], y[:, :-1])
+    assert int(x.min()) >= 0 and int(x.max()) < 16384
+    counts = np.bincount(x.flatten().numpy(), minlength=16384)
+    p1 = 1.0 / sum(k ** -1.1 for k in range(1, 16385))
+    assert abs(counts[0] / x.numel() - p1) < 0.03  # rank 1 carries ~10% of the mass
+    assert counts[0] > counts[1] > counts[10]
