@@ -15,18 +15,19 @@
 // backward consumes Q_rot / K_rot directly and rotates dQ / dK back by -theta
 // in its epilogues (src/mega_trading/kernels/triton_ops.py:205-214).
 //
-// Tiling.  A "row block" is 64 query rows of one head, a "KV tile" 64 keys.
+// Tiling.  A "row block" is 64 query rows of one head.
 //   * forward / dQ: a workgroup is 4 waves; each wave owns one (query head,
 //     row block).  The 4 waves are the R_SUB = min(R, 4) heads of one KV group
 //     times 4/R_SUB consecutive row blocks, so every K/V tile staged in LDS
-//     feeds all of them.  S^T = K Q^T puts one query per lane (lane % 32),
+//     feeds all of them (forward: 128-key tiles, dQ: 64-key tiles, both
+//     double-buffered).  S^T = K Q^T puts one query per lane (lane % 32),
 //     keys along the accumulator slots; the row max needs one lane^32 swap.
-//   * dK/dV: a workgroup is 2 waves; each owns KPW keys of one KV head and
-//     walks (query head, row block on or below the diagonal) steps, with the
-//     Q / dO tiles of each step staged in LDS once for both waves.  The
-//     group's heads may be split over several workgroups (fp32 partial sums,
-//     combined by attn_bwd_combine_kernel) so the causal triangle spreads over
-//     enough workgroups to balance.
+//   * dK/dV: a workgroup is 4 waves of 32 keys each (a 128-key block of one
+//     KV head, K and V held in registers); it walks (query head, 128-row step
+//     on or below the diagonal) with the Q / dO rows of each step staged in
+//     LDS once for all 4 waves.  The group's heads may be split over several
+//     workgroups (fp32 partial sums, combined by attn_bwd_combine_kernel) so
+//     the causal triangle spreads over enough workgroups to balance.
 // Fully masked causal tiles are never visited; only diagonal tiles mask.
 #pragma once
 
@@ -35,7 +36,7 @@
 
 namespace mt {
 
-constexpr int kBlk = 64;   // rows per row block == keys per KV tile
+constexpr int kBlk = 64;   // rows per row block (and keys per dQ K/V tile)
 
 struct AttnParams {
   // [B, H, T, D] tensors, element strides (b, h, t); the d stride is 1.
