@@ -151,31 +151,28 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t* x, int64
 // ===========================================================================
 // Forward
 // ===========================================================================
-// Lazy rescaling: the running row max m used as the exponent offset is only
-// raised when a quarter's max exceeds it by more than kRescaleSlack (log2
-// units), so P = 2^(s*c - m) stays below 2^kRescaleSlack (fits fp16 too) and
-// most quarters skip the O / l rescale.  O = acc / l and LSE = (m + log2 l)
-// ln 2 are exact for any m, so the result does not depend on when rescales
-// happen.
+// Lazy rescaling: the running row offset m (log2 units) is only raised when a
+// quarter's probabilities P = 2^(s*c - m) may exceed 2^kRescaleSlack, which is
+// detected from the quarter's row sums (any P above the bound makes the sum
+// exceed it; a NaN sum -- the first quarter, with m = -inf -- also fails the
+// test).  The row max is computed only then, O and l are rescaled and the
+// quarter's P recomputed.  P stays below 2^kRescaleSlack (fits fp16 too), and
+// O = acc / l and LSE = (m + log2 l) ln 2 are exact for any m, so the result
+// does not depend on when rescales happen.  Row sums add the packed 16-bit P
+// (v_dot2c with 1.0, 1.0), i.e. exactly the weights the PV product uses.
 constexpr float kRescaleSlack = 8.0f;
+constexpr float kSumLimit = 256.0f;  // 2^kRescaleSlack
 constexpr int kFwdKeys = 128;  // keys per staged K/V tile (two 64-row halves)
-
-// Multiply 8 packed 16-bit values by a scalar (rare path: rescaling a
-// quarter's P after the offset moved).
-template <class E>
-__device__ __forceinline__ typename E::v8 scale8(typename E::v8 x, float a) {
-  const u32x4 w = __builtin_bit_cast(u32x4, x);
-  u32x4 r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) r[p] = pack2<E>(lo_f<E>(w[p]) * a, hi_f<E>(w[p]) * a);
-  return __builtin_bit_cast(typename E::v8, r);
-}
+#ifndef MT_FWD_VALU_PER_MFMA
+#define MT_FWD_VALU_PER_MFMA 0
+#endif
+constexpr int kFwdValuPerMfma = MT_FWD_VALU_PER_MFMA;  // E(h) VALU slots after each MFMA
 
 // One 128-key tile for one wave (64 query rows, two 32-row column tiles nt).
 // Quarter h = keys kt0 + 32h .. +31.  Pipeline (issue order):
-//   S0 | M0 | S1 + E0 | M1 | PV0 + S2 + E1 | M2 | PV1 + S3 + E2 | M3 | PV2 + E3 | PV3
-// Sh = scores of quarter h, Mh = its row max and (rare, wave-uniform)
-// rescale branch, Eh = its exponentials / row sums / packing, PVh = O += P V.
+//   S0 | S1 + E0 | C0 | PV0 + S2 + E1 | C1 | PV1 + S3 + E2 | C2 | PV2 + E3 | C3 | PV3
+// Sh = scores of quarter h, Eh = its exponentials, packing and row sums,
+// Ch = the overflow test and (rare, wave-uniform) rescale, PVh = O += P V.
 // With MASK (the tile holding this wave's diagonal) keys above the query are
 // masked and quarters wholly above the wave's rows are skipped.
 template <class E, int D, bool MASK>
@@ -205,32 +202,47 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
       for (int nt = 0; nt < 2; ++nt) st[nt] = E::mfma(a, qop[nt][kk], st[nt]);
     }
   };
-  // row max + rescale decision; `prev` = the previous quarter's packed P
-  // (still to be multiplied into O), rescaled with O when the offset moves
-  auto mx = [&](int h, f32x16* st, V8 (*prev)[2], bool has_prev) {
-    if constexpr (MASK) {
+  // P = 2^(S c2 - m) packed to 16 bits (S kept for a possible rescale);
+  // qs = this lane's share of the quarter's row sums
+  auto ex = [&](int h, f32x16* st, V8 (*pk)[2], float* qs) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < 2; ++nt) {
+      if constexpr (MASK) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int kr = kt0 + 32 * h + 8 * (i >> 2) + 4 * hh + (i & 3);
           if (kr > q0 + 32 * nt + l32) st[nt][i] = -INFINITY;
         }
-    }
-    float m[2];
-    bool need = false;
+      }
+      const float moff = mrun[nt];
+      u32x4 w[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      float v = -INFINITY;
+      for (int p2 = 0; p2 < 8; ++p2) {
+        const float a = exp2_fast(__builtin_fmaf(st[nt][2 * p2], c2, -moff));
+        const float b = exp2_fast(__builtin_fmaf(st[nt][2 * p2 + 1], c2, -moff));
+        w[p2 >> 2][p2 & 3] = pack2<E>(a, b);
+      }
+      float s0 = E::sum2(w[0][0], 0.f), s1 = E::sum2(w[1][0], 0.f);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v = fmaxf(v, st[nt][i]);
-      m[nt] = max_with_partner(v) * c2;
-      need |= m[nt] > mrun[nt] + kRescaleSlack;
+      for (int p = 1; p < 4; ++p) {
+        s0 = E::sum2(w[0][p], s0);
+        s1 = E::sum2(w[1][p], s1);
+      }
+      qs[nt] = s0 + s1;
+      pk[nt][0] = __builtin_bit_cast(V8, w[0]);
+      pk[nt][1] = __builtin_bit_cast(V8, w[1]);
     }
-    if (__builtin_amdgcn_ballot_w64(need)) {
+  };
+  // overflow test; on failure raise m to the row max, rescale O and l, redo E
+  auto chk = [&](int h, f32x16* st, V8 (*pk)[2], float* qs) {
+    const bool bad = !(qs[0] <= kSumLimit) || !(qs[1] <= kSumLimit);
+    if (__builtin_amdgcn_ballot_w64(bad)) {
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        const float mnew = fmaxf(mrun[nt], m[nt]);
+        float v = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v = fmaxf(v, st[nt][i]);
+        const float mnew = fmaxf(mrun[nt], max_with_partner(v) * c2);
         const float alpha = exp2_fast(mrun[nt] - mnew);
         mrun[nt] = mnew;
         lrun[nt] *= alpha;
@@ -238,28 +250,11 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int i = 0; i < 16; ++i) oacc[dt][nt][i] *= alpha;
-        if (has_prev) {
-          prev[nt][0] = scale8<E>(prev[nt][0], alpha);
-          prev[nt][1] = scale8<E>(prev[nt][1], alpha);
-        }
       }
+      ex(h, st, pk, qs);
     }
-  };
-  auto ex = [&](f32x16* st, V8 (*pk)[2]) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const float moff = mrun[nt];
-      float ls[4];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pv = exp2_fast(__builtin_fmaf(st[nt][i], c2, -moff));
-        st[nt][i] = pv;
-        ls[i & 3] = i < 4 ? pv : ls[i & 3] + pv;
-      }
-      lrun[nt] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-      pk[nt][0] = pack8<E>(st[nt], 0);
-      pk[nt][1] = pack8<E>(st[nt], 8);
-    }
+    lrun[0] += qs[0];
+    lrun[1] += qs[1];
   };
   auto pv = [&](int h, V8 (*pk)[2]) {
     const char* Vh = Vt + (h >> 1) * TL::BYTES;
@@ -272,11 +267,11 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
         for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pk[nt][k2], oacc[dt][nt]);
       }
   };
-  constexpr int NS = 2 * KT;       // S MFMAs of a quarter
   constexpr int NP = 4 * DT;       // PV MFMAs of a quarter
 
   f32x16 st[2][2];                 // ring: two quarters' scores [slot][nt]
   V8 pk[2][2][2];                  // ring: two quarters' packed P [slot][nt][k2]
+  float qs[2];
   // LDS operand reads run one step ahead of the MFMAs that consume them
   if (live[0]) sq(0, st[0]);
   __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -288,38 +283,39 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
-    // M(h): needs S(h); may rescale the pending P(h-1)
-    if (live[h]) mx(h, st[h & 1], pk[(h + 1) & 1], h > 0 && live[h - 1]);
-    __builtin_amdgcn_sched_barrier(0);
     // region: PV(h-1) + S(h+1) MFMAs interleaved with E(h)
     if (h > 0 && live[h - 1]) pv(h - 1, pk[(h + 1) & 1]);
     if (h < 3 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
-    if (live[h]) ex(st[h & 1], pk[h & 1]);
-    constexpr int dummy = 0;
-    (void)dummy;
-    if (h > 0) {
+    if (live[h]) ex(h, st[h & 1], pk[h & 1], qs);
+    // each MFMA followed by kFwdValuPerMfma VALU instructions of E(h); every
+    // operand read is issued one operand (two MFMAs) ahead
+    if (kFwdValuPerMfma == 0) {
+      // leave the interleaving to the scheduler
+    } else if (h > 0) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-      for (int i = 0; i < NP / 2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+      for (int i = 0; i < NP; ++i) {
+        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kFwdValuPerMfma, 0);
       }
     } else {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    if (h < 3) {
+    if (kFwdValuPerMfma > 0 && h < 3) {
 #pragma unroll
-      for (int i = 0; i < KT; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+      for (int i = 0; i < 2 * KT; ++i) {
+        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kFwdValuPerMfma, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // C(h): after PV(h-1), so a rescale of O covers everything accumulated
+    if (live[h]) chk(h, st[h & 1], pk[h & 1], qs);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (live[3]) pv(3, pk[1]);
-  (void)NS;
 }
 
 template <class E, int D, bool ROPE>
@@ -634,6 +630,14 @@ __device__ __forceinline__ void softmax_dS32(f32x16& s, f32x16& dp, const float*
 // ===========================================================================
 // Backward, dK / dV
 // ===========================================================================
+#ifndef MT_DKV_GROUPS
+#define MT_DKV_GROUPS 0
+#endif
+// explicit MFMA / VALU / LDS-read interleaving of the dK/dV step (0: scheduler's choice)
+#define MT_DKV_GROUP(mask, n) \
+  do {                       \
+    if constexpr (MT_DKV_GROUPS) __builtin_amdgcn_sched_group_barrier(mask, n, 0); \
+  } while (0)
 constexpr int kKvWaves = 4;    // waves per dK/dV workgroup
 constexpr int kKvKpw = 32;     // keys per wave
 constexpr int kKvKeys = kKvWaves * kKvKpw;
@@ -702,8 +706,8 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
   if (live[0]) sdp(0, s[0], dp[0]);
 #pragma unroll
   for (int i = 0; i < KT; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    MT_DKV_GROUP(0x100, 2);
+    MT_DKV_GROUP(0x008, 2);
   }
   __builtin_amdgcn_sched_barrier(0);
   // phase 2: SdP1 + V0
@@ -711,9 +715,9 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
   if (live[0]) vh(0, s[0], dp[0], pk[0], dk[0]);
 #pragma unroll
   for (int i = 0; i < KT; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+    MT_DKV_GROUP(0x100, 2);
+    MT_DKV_GROUP(0x008, 2);
+    MT_DKV_GROUP(0x002, 16);
   }
   __builtin_amdgcn_sched_barrier(0);
   // phases 3, 4: dVdK(h-2) + SdP(h) + V(h-1), h = 2, 3
@@ -724,15 +728,15 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
     if (live[h - 1]) vh(h - 1, s[(h - 1) & 1], dp[(h - 1) & 1], pk[(h - 1) & 1], dk[(h - 1) & 1]);
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      MT_DKV_GROUP(0x100, 2);
+      MT_DKV_GROUP(0x008, 1);
+      MT_DKV_GROUP(0x002, 6);
     }
 #pragma unroll
     for (int i = 0; i < KT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      MT_DKV_GROUP(0x100, 2);
+      MT_DKV_GROUP(0x008, 2);
+      MT_DKV_GROUP(0x002, 6);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -741,17 +745,17 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
   if (live[3]) vh(3, s[1], dp[1], pk[1], dk[1]);
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, 10, 0);
+    MT_DKV_GROUP(0x100, 2);
+    MT_DKV_GROUP(0x008, 1);
+    MT_DKV_GROUP(0x002, 10);
   }
   __builtin_amdgcn_sched_barrier(0);
   // phase 6: dVdK3
   if (live[3]) dvdk(3, pk[1], dk[1]);
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    MT_DKV_GROUP(0x100, 2);
+    MT_DKV_GROUP(0x008, 1);
   }
   (void)NS;
 }

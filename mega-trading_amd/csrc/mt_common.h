@@ -41,6 +41,11 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_f(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+  // acc + lo(w) + hi(w) for two packed values (v_dot2c_f32_bf16 against 1.0, 1.0)
+  static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                           acc, false);
+  }
 };
 
 struct FP16 {
@@ -52,6 +57,9 @@ struct FP16 {
   }
   static __device__ __forceinline__ float to_f(uint16_t x) {
     return (float)__builtin_bit_cast(_Float16, x);
+  }
+  static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
   }
 };
 
