@@ -177,7 +177,7 @@ constexpr int kFwdValuPerMfma = MT_FWD_VALU_PER_MFMA;  // E(h) VALU slots after 
 // masked and quarters wholly above the wave's rows are skipped.
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const typename E::v8 (*qop)[D / 16],
-                                         f32x16 (*oacc)[2], float* mrun, float* lrun, int rbase, int tbase,
+                                         f32x16 (*oacc)[2], float* mrun, float* lrun, int rbase, TrBase tbase,
                                          int lane, int kt0, int q0, float c2) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   ks_stage.init(p.sk[2], wave, lane);
   vs_stage.init(p.sv[2], wave, lane);
   const int rbase_op = TL::row_base(lane);
-  const int tbase_op = TL::tr_base(lane);
+  const TrBase tbase_op = TL::tr_base(lane);
   auto stage = [&](int j, int buf) {
     const int r0 = j * kFwdKeys;
     ks_stage.stage(smem[buf][0], kbase, p.sk[2], r0, p.T);
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
   ks_stage.init(p.sk[2], wave, lane);
   vs_stage.init(p.sv[2], wave, lane);
   const int rbase_op = TL::row_base(lane);
-  const int tbase_op = TL::tr_base(lane);
+  const TrBase tbase_op = TL::tr_base(lane);
 
   ks_stage.stage(smem[0][0], kbase, p.sk[2], 0, p.T);
   vs_stage.stage(smem[0][1], vbase, p.sv[2], 0, p.T);
@@ -654,7 +654,7 @@ constexpr int kKvRows = 128;   // query rows staged per step (two row blocks)
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const float* lrow, const float* drow,
                                          const typename E::v8* kop, const typename E::v8* vop,
-                                         f32x16* dkacc, f32x16* dvacc, int rbase, int tbase, int lane,
+                                         f32x16* dkacc, f32x16* dvacc, int rbase, TrBase tbase, int lane,
                                          int key, int k0, int qrow0, int T, float c2) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
@@ -815,7 +815,7 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   qs_stage.init(p.sq[2], wave, lane);
   gs_stage.init(p.sdo[2], wave, lane);
   const int rbase_op = TL::row_base(lane);
-  const int tbase_op = TL::tr_base(lane);
+  const TrBase tbase_op = TL::tr_base(lane);
 
   // (head, first row) of a step, advanced without divisions
   auto stage = [&](int head, int row0, int buf) {

@@ -1,13 +1,19 @@
 // LDS tiles of 64 rows x D 16-bit elements for the gfx950 attention kernels.
 //
 // Layout: rows are stored unpadded (RB = 2*D bytes); the 16-byte chunks of
-// row r are XOR-swizzled, chunk c living at slot c ^ f(r).  For 8 chunks per
-// row and more, f(r) = 2*(r%4) + (r/4)%2: the 8 lanes of a ds_read_b128 phase
-// (one chunk column of 8 consecutive rows) hit 8 different slots, and the 16
-// lanes of a ds_read_b64_tr_b16 phase (4 consecutive rows x 2 neighbouring
-// chunks) hit 8 different slots too.  Because the swizzle is an XOR with bits
-// the operand offsets never touch, every operand address is a per-lane base
-// computed once, XOR-ed with a per-step constant, plus an immediate row offset.
+// row r are XOR-swizzled, chunk c living at slot c ^ f(r), f of period 16.
+// The gfx950 LDS serves 256 bytes per clock: a wave's ds_read_b128 is served
+// 16 lanes at a time and a ds_read_b64_tr_b16 32 lanes at a time, so an
+// access is conflict-free when each such group covers 256 distinct bytes
+// modulo 256.  For D = 64 (two rows per 256 bytes) f(r) = 4*((r/2) % 2) +
+// (r/4) % 4 makes the 16 consecutive rows of a ds_read_b128 group (one chunk
+// column) and the 4 rows x 4 chunks of a transposed-read group land on 16
+// distinct 16-byte slots; for D = 128 (one row per 256 bytes) f(r) =
+// 4*(r % 4) + (r/4) % 4 does the same, and for D = 32 (four rows per 256
+// bytes) f(r) = (r/4) % 4.  Because the swizzle is an XOR with
+// bits the operand offsets never touch and has period 16, every operand
+// address is a per-lane base computed once, XOR-ed with a per-step constant,
+// plus an immediate offset of a multiple of 16 rows.
 //
 // Staging uses global_load_lds_dwordx4: each lane of a wave copies 16 bytes
 // from its own global address straight into LDS at (wave base + 16 * lane),
@@ -21,7 +27,8 @@
 //             (one ds_read_b128 per lane).
 //  * tr_op:   A operand with M = tile columns, k = tile rows in the permuted
 //             order 16*ks + 8*(j/4) + 4*h + (j%4) that matches a C tile fed
-//             back as a B operand (two ds_read_b64_tr_b16 per lane).
+//             back as a B operand (two ds_read_b64_tr_b16 per lane, rows
+//             16ks + 0..7 and 16ks + 8..15, from two per-lane bases).
 //             ds_read_b64_tr_b16 semantics (measured on gfx950): in each
 //             16-lane group, output lane i element e is element (i % 4) of the
 //             8 bytes addressed by lane 4*e + i/4 of the group.  Lane j of the
@@ -36,18 +43,24 @@ namespace mt {
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
+// Per-lane bases of the two transposed reads of a tr_op (rows 0..7 and 8..15
+// of a 16-row group).
+struct TrBase {
+  int lo, hi;
+};
+
 template <int D>
 struct Tile {
   static constexpr int NC = D / 8;              // 16-byte chunks per row
-  static constexpr int SW = NC < 8 ? NC : 8;    // swizzle period
   static constexpr int RB = 2 * D;              // row bytes
   static constexpr int BYTES = 64 * RB;         // one 64-row tile
   static constexpr int INSTR = NC;              // 1 KB wave instructions per tile (64 * NC * 16 B / 1 KB)
 
-  // slot permutation of row r (depends on r % 8 only)
+  // slot permutation of row r (period 16)
   static __device__ __forceinline__ int swz(int row) {
-    if constexpr (SW == 8) return ((row & 3) << 1) | ((row >> 2) & 1);
-    return row % SW;
+    if constexpr (NC == 8) return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+    else if constexpr (NC == 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+    else return (row >> 2) & 3;  // NC == 4: four rows per 256 bytes
   }
 
   // --- operand addressing -------------------------------------------------
@@ -57,13 +70,14 @@ struct Tile {
     const int chunk = lane >> 5;
     return row * RB + ((chunk ^ swz(row)) << 4);
   }
-  // tr_op base: lane's 8-byte source at r0 = 0, c0 = 0 (first of the two reads).
-  static __device__ __forceinline__ int tr_base(int lane) {
+  // tr_op bases: lane's 8-byte source in rows 0..7 and 8..15 at c0 = 0.
+  static __device__ __forceinline__ TrBase tr_base(int lane) {
     const int g = lane >> 4;
     const int i = lane & 15;
     const int row = 4 * (g >> 1) + (i >> 2);
     const int col = 16 * (g & 1) + 4 * (i & 3);
-    return row * RB + (((col >> 3) ^ swz(row)) << 4) + ((col & 7) << 1);
+    auto at = [&](int r) { return r * RB + (((col >> 3) ^ swz(r)) << 4) + ((col & 7) << 1); };
+    return TrBase{at(row), at(row + 8)};
   }
 
   template <class E>
@@ -72,10 +86,10 @@ struct Tile {
   }
 
   template <class E>
-  static __device__ __forceinline__ typename E::v8 tr_op(const char* lds, int base, int ks, int dt) {
-    const char* p = lds + (base ^ (64 * dt)) + 16 * ks * RB;
-    i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p);
-    i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * RB));
+  static __device__ __forceinline__ typename E::v8 tr_op(const char* lds, TrBase b, int ks, int dt) {
+    const char* p = lds + 16 * ks * RB;
+    i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + (b.lo ^ (64 * dt))));
+    i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + (b.hi ^ (64 * dt))));
     u32x4 w = {__builtin_bit_cast(u32x2, lo)[0], __builtin_bit_cast(u32x2, lo)[1],
                __builtin_bit_cast(u32x2, hi)[0], __builtin_bit_cast(u32x2, hi)[1]};
     return __builtin_bit_cast(typename E::v8, w);
