@@ -438,6 +438,66 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
 // ===========================================================================
 // Backward, dQ (also writes delta = rowsum(O * dO))
 // ===========================================================================
+// One 64-key K/V tile against the wave's 64 query rows: S^T and dP^T
+// recomputed (lane = query), P = 2^(S c2 - lse2), dS = P (dP - delta),
+// dQ += dS K.  With MASK (the diagonal tile) keys above the query get P = 0.
+template <class E, int D, bool MASK>
+__device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typename E::v8 (*qop)[D / 16],
+                                        const typename E::v8 (*gop)[D / 16], f32x16 (*dqacc)[2], const float* lse2,
+                                        const float* dlt, int rbase, TrBase tbase, int l32, int hh, float c2) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+  // the two 32-query halves one after the other keeps S/dP at 64 VGPRs
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    f32x16 st[2], dpt[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      {
+        const V8 a = TL::template row_op<E>(K, rbase, mt * 32, 0);
+        const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
+        st[mt] = E::mfma(a, qop[nt][0], f32x16{});
+        dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
+      }
+#pragma unroll
+      for (int kk = 1; kk < KT; ++kk) {
+        const V8 a = TL::template row_op<E>(K, rbase, mt * 32, kk);
+        const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, kk);
+        st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
+        dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      V8 dsb[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
+        if constexpr (MASK) {
+          const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if (kr > nt * 32 + l32) pv = 0.f;
+        }
+        st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
+      }
+      dsb[0] = pack8<E>(st[mt], 0);
+      dsb[1] = pack8<E>(st[mt], 8);
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const V8 a = TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt);
+          dqacc[dt][nt] = E::mfma(a, dsb[k2], dqacc[dt][nt]);
+        }
+      }
+    }
+    // keep the two halves' live ranges apart (the scheduler would
+    // otherwise interleave them and exceed the register budget)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 template <class E, int D, bool ROPE>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnParams p) {
   using V8 = typename E::v8;
@@ -519,55 +579,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
       vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
     }
     if (active && j <= qb) {
-      const char* K = smem[buf][0];
-      const char* Vr = smem[buf][1];
-      // the two 32-query halves one after the other keeps S/dP at 64 VGPRs
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        f32x16 st[2], dpt[2];
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          {
-            const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, 0);
-            const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, 0);
-            st[mt] = E::mfma(a, qop[nt][0], f32x16{});
-            dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
-          }
-#pragma unroll
-          for (int kk = 1; kk < KT; ++kk) {
-            const V8 a = TL::template row_op<E>(K, rbase_op, mt * 32, kk);
-            const V8 b = TL::template row_op<E>(Vr, rbase_op, mt * 32, kk);
-            st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
-            dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
-          }
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          V8 dsb[2];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
-            if (j == qb) {
-              const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-              if (kr > nt * 32 + l32) pv = 0.f;
-            }
-            st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
-          }
-          dsb[0] = pack8<E>(st[mt], 0);
-          dsb[1] = pack8<E>(st[mt], 8);
-#pragma unroll
-          for (int k2 = 0; k2 < 2; ++k2) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              const V8 a = TL::template tr_op<E>(K, tbase_op, 2 * mt + k2, dt);
-              dqacc[dt][nt] = E::mfma(a, dsb[k2], dqacc[dt][nt]);
-            }
-          }
-        }
-        // keep the two halves' live ranges apart (the scheduler would
-        // otherwise interleave them and exceed the register budget)
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      if (j < qb)
+        dq_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh, c2);
+      else
+        dq_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh, c2);
     }
     wait_vmem();
     __syncthreads();
