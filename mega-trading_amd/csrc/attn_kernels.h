@@ -498,7 +498,11 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
   }
 }
 
-template <class E, int D, bool ROPE>
+// PEEL: the workgroup's 4 waves are 4 heads of one row block, so every active
+// wave's diagonal tile is the workgroup's last tile and is handled after the
+// loop; keeping the masked tile out of the loop keeps the loop within the
+// register budget.
+template <class E, int D, bool ROPE, bool PEEL>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
@@ -572,14 +576,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
   __syncthreads();
 
   const float c2 = p.scale_log2;
-  for (int j = 0; j <= jlast; ++j) {
+  for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
     const int buf = j & 1;
     if (j < jlast) {
       ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
       vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
     }
     if (active && j <= qb) {
-      if (j < qb)
+      if (PEEL || j < qb)
         dq_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh, c2);
       else
         dq_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh, c2);
@@ -587,6 +591,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
     wait_vmem();
     __syncthreads();
   }
+  if (PEEL && active)  // qb == jlast
+    dq_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32,
+                        hh, c2);
 
   if (!active) return;
   uint16_t* dqbase = p.out + task.b * p.sout[0] + (int64_t)head * p.sout[1];
