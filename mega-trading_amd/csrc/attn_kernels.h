@@ -318,7 +318,9 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
   if (live[3]) pv(3, pk[1]);
 }
 
-template <class E, int D, bool ROPE>
+// PEEL: as for the dQ kernel, the 4 waves share one row block, so the
+// diagonal (masked) tile is the last one and runs after the loop.
+template <class E, int D, bool ROPE, bool PEEL>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
@@ -397,11 +399,11 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   __syncthreads();
 
   const float c2 = p.scale_log2;
-  for (int j = 0; j <= jlast; ++j) {
+  for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
     const int buf = j & 1;
     if (j < jlast) stage(j + 1, buf ^ 1);
     if (active && j <= jw) {
-      if (j < jw)
+      if (PEEL || j < jw)
         fwd_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
                               j * kFwdKeys, q0, c2);
       else
@@ -411,6 +413,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
     wait_vmem();
     __syncthreads();
   }
+  if (PEEL && active)  // jw == jlast
+    fwd_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                         jlast * kFwdKeys, q0, c2);
 
   if (!active) return;
   uint16_t* obase = p.out + task.b * p.so[0] + (int64_t)head * p.so[1];
