@@ -348,10 +348,25 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
   const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
 
   // Q^T as B operands (N = query, k = d), rotated if RoPE (and written out).
+  // Every load is issued before the first use and the first Q_rot store, so
+  // the prologue costs one memory round trip (rows past T load row T-1 and
+  // are zeroed).
   V8 qop[2][KT];
   {
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     uint16_t* rbase = ROPE ? p.qrot + ((int64_t)task.b * p.Hq + head) * p.T * D : nullptr;
+    u32x4 x[2][KT];
+    f32x4 cs[2][ROPE ? KT : 1], sn[2][ROPE ? KT : 1];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int rc = min(q0 + nt * 32 + l32, p.T - 1);
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        const int d0 = 16 * kk + 8 * hh;
+        x[nt][kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
+        if constexpr (ROPE) load_rope_cs<D>(p.cos, p.sin, rc, d0, cs[nt][kk], sn[nt][kk]);
+      }
+    }
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int row = q0 + nt * 32 + l32;
@@ -359,16 +374,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
         const int d0 = 16 * kk + 8 * hh;
-        u32x4 x = ok ? load_chunk(qbase, p.sq[2], row, p.T, d0) : zero4();
+        u32x4 y = ok ? x[nt][kk] : zero4();
         if constexpr (ROPE) {
-          if (ok) {
-            f32x4 c, s;
-            load_rope_cs<D>(p.cos, p.sin, row, d0, c, s);
-            x = rope_chunk<E>(x, c, s);
-            *reinterpret_cast<u32x4*>(rbase + (int64_t)row * D + d0) = x;
-          }
+          y = rope_chunk<E>(y, cs[nt][kk], sn[nt][kk]);
+          if (ok) *reinterpret_cast<u32x4*>(rbase + (int64_t)row * D + d0) = y;
         }
-        qop[nt][kk] = __builtin_bit_cast(V8, x);
+        qop[nt][kk] = __builtin_bit_cast(V8, y);
       }
     }
   }
@@ -537,6 +548,22 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     const uint16_t* gbase = p.dout + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
     const uint16_t* obase = p.o + task.b * p.so[0] + (int64_t)head * p.so[1];
+    // all loads first (one memory round trip; rows past T load row T-1 and
+    // are zeroed), then delta and the stores
+    u32x4 qx[2][KT], gx[2][KT], ox[2][KT];
+    float lx[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int rc = min(q0 + nt * 32 + l32, p.T - 1);
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        const int d0 = 16 * kk + 8 * hh;
+        qx[nt][kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
+        gx[nt][kk] = *reinterpret_cast<const u32x4*>(gbase + (int64_t)rc * p.sdo[2] + d0);
+        ox[nt][kk] = *reinterpret_cast<const u32x4*>(obase + (int64_t)rc * p.so[2] + d0);
+      }
+      lx[nt] = p.lse[rowbase + rc];
+    }
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int row = q0 + nt * 32 + l32;
@@ -544,10 +571,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
       float dsum = 0.f;
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
-        const int d0 = 16 * kk + 8 * hh;
-        qop[nt][kk] = __builtin_bit_cast(V8, ok ? load_chunk(qbase, p.sq[2], row, p.T, d0) : zero4());
-        const u32x4 g = ok ? load_chunk(gbase, p.sdo[2], row, p.T, d0) : zero4();
-        const u32x4 o = ok ? load_chunk(obase, p.so[2], row, p.T, d0) : zero4();
+        qop[nt][kk] = __builtin_bit_cast(V8, ok ? qx[nt][kk] : zero4());
+        const u32x4 g = ok ? gx[nt][kk] : zero4();
+        const u32x4 o = ox[nt][kk];
         gop[nt][kk] = __builtin_bit_cast(V8, g);
 #pragma unroll
         for (int w = 0; w < 4; ++w)
@@ -555,7 +581,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
       }
       dsum = sum_with_partner(dsum);
       dlt[nt] = dsum;
-      lse2[nt] = ok ? p.lse[rowbase + row] * kLog2e : 0.f;
+      lse2[nt] = ok ? lx[nt] * kLog2e : 0.f;
       if (ok && hh == 0) {
         p.delta[rowbase + row] = dsum;
         p.lse2[rowbase + row] = lse2[nt];
