@@ -1,8 +1,10 @@
-"""Build libmt_attn.so in-tree for gfx950 with hipcc.
+"""Build libmt_attn.so (and the bench-only libmt_probe.so) in-tree for gfx950 with hipcc.
 
 Run as ``python mega-trading_amd/build_lib.py`` or through
-``__graft_entry__.build()``.  The library lands next to this file so it
-travels with the source tree (it is git-ignored, not installed anywhere).
+``__graft_entry__.build()``.  The libraries land next to this file so they
+travel with the source tree (they are git-ignored, not installed anywhere).
+libmt_probe.so holds a sustained-MFMA-rate probe that bench.py reports beside
+the roofline; it is not part of the attention ABI.
 """
 
 from __future__ import annotations
@@ -17,6 +19,9 @@ CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libmt_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["mt_attention.hip"]
+PROBE_NAME = "libmt_probe.so"
+PROBE_PATH = os.path.join(HERE, PROBE_NAME)
+PROBE_SOURCES = ["mfma_probe.hip"]
 HEADERS = ["mt_common.h", "attn_kernels.h"]
 ARCH = "gfx950"
 
@@ -28,7 +33,7 @@ def hipcc() -> str:
     return path
 
 
-def compile_command(out: str = LIB_PATH) -> list[str]:
+def compile_command(out: str = LIB_PATH, sources: list[str] | None = None) -> list[str]:
     return [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -40,14 +45,19 @@ def compile_command(out: str = LIB_PATH) -> list[str]:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-pass-failed",
         "-o", out,
-        *[os.path.join(CSRC, s) for s in SOURCES],
+        *[os.path.join(CSRC, s) for s in (SOURCES if sources is None else sources)],
     ]
 
 
 def build(verbose: bool = False) -> str:
-    """Compile the library (always; a stale build is never reused)."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = compile_command(tmp)
+    """Compile both libraries (always; a stale build is never reused)."""
+    _compile(PROBE_PATH, PROBE_SOURCES, verbose)
+    return _compile(LIB_PATH, SOURCES, verbose)
+
+
+def _compile(path: str, sources: list[str], verbose: bool) -> str:
+    tmp = path + ".tmp"
+    cmd = compile_command(tmp, sources)
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,8 +67,8 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, path)
+    return path
 
 
 if __name__ == "__main__":

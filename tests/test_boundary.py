@@ -33,6 +33,15 @@ def test_library_exports_every_declared_symbol(mta):
     assert lib.mt_version() == (0 << 16) | 3
 
 
+def test_probe_library_exports_the_mfma_probe():
+    # bench.py's sustained-MFMA probe lives in its own library, outside the attention ABI
+    path = os.path.join(ROOT, "mega-trading_amd", "libmt_probe.so")
+    assert os.path.exists(path), "run mega-trading_amd/build_lib.py"
+    lib = ctypes.CDLL(path)
+    assert hasattr(lib, "mt_probe_mfma")
+    assert b"gfx950" in open(path, "rb").read()
+
+
 def test_library_is_gfx950_only(mta):
     data = open(mta._native.library_path(), "rb").read()
     assert b"gfx950" in data
