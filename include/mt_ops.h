@@ -1,0 +1,84 @@
+/*
+ * C ABI of the decoder operators around the attention (also in
+ * libmt_attn.so): RMSNorm, residual-add + RMSNorm and the SwiGLU gate,
+ * forward and backward, for MI355X (gfx950).  Plain pointers and sizes only.
+ *
+ * They replace these reference operators (src/mega_trading/kernels/triton_ops.py):
+ *
+ *   mt_rms_norm_fwd      <- _TritonRMSNorm.forward :135-156 (kernel :528-539),
+ *                           reached from triton_rms_norm :11-15 and
+ *                           RMSNorm.forward, src/mega_trading/model.py:267-268
+ *   mt_rms_norm_bwd      <- _TritonRMSNorm.backward :158-184 (kernel :633-666,
+ *                           dW = partial_weight.sum(dim=0) :183)
+ *   mt_add_rms_norm_fwd  <- _TritonAddRMSNorm.forward :219-249 (kernel :541-566),
+ *                           reached from triton_add_rms_norm :18-42
+ *   mt_add_rms_norm_bwd  <- _TritonAddRMSNorm.backward :251-291 (kernel :569-608)
+ *   mt_swiglu_fwd        <- _TritonSwiGLUGate.forward :433-453 (kernel :774-782),
+ *                           reached from triton_swiglu_gate :57-61 and
+ *                           SwiGLU.forward, src/mega_trading/model.py:252-253
+ *   mt_swiglu_bwd        <- _TritonSwiGLUGate.backward :455-474 (kernel :799-819)
+ *
+ * Conventions (as in mt_attention.h): device pointers on the current device,
+ * asynchronous on `stream`, no allocation, no synchronisation; 0 = success,
+ * negative = argument error (MT_E_*), positive = hipError_t; the message is in
+ * mt_last_error().
+ *
+ *   - dtype / weight_dtype: MT_DTYPE_BF16, MT_DTYPE_FP16 or MT_DTYPE_FP32;
+ *     weight_dtype is either dtype or MT_DTYPE_FP32.  Arithmetic is fp32.
+ *   - RMSNorm rows: x is [rows, dim] with row stride x_row_stride (elements,
+ *     last stride 1); every other [rows, dim] tensor is contiguous.
+ *     dim % 8 == 0 and 8 <= dim <= 4096; base pointers and row starts
+ *     16-byte aligned.  rstd is fp32 [rows]: 1 / sqrt(mean(x^2) + eps).
+ *   - SwiGLU: n values, contiguous, 16-byte aligned, any n >= 0.
+ */
+#ifndef MT_OPS_H_
+#define MT_OPS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mt_attention.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MT_DTYPE_FP32 2
+
+/* y = x * rstd * weight; rstd written per row. */
+int mt_rms_norm_fwd(const void* x, int64_t x_row_stride, const void* weight, void* y, float* rstd, int64_t rows,
+                    int dim, float eps, int dtype, int weight_dtype, void* stream);
+
+/* new_residual = x + residual (stored in dtype), y = RMSNorm(new_residual) computed
+ * from the unrounded fp32 sum; rstd written per row. */
+int mt_add_rms_norm_fwd(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                        const void* weight, void* new_residual, void* y, float* rstd, int64_t rows, int dim,
+                        float eps, int dtype, int weight_dtype, void* stream);
+
+/* Bytes of fp32 workspace the RMSNorm backward needs (per-workgroup dW partial rows). */
+size_t mt_rms_norm_bwd_workspace_size(int64_t rows, int dim);
+
+/* dx = rstd (dy w - x rstd^2 / dim * sum(dy w x)); dweight = sum over rows of dy x rstd
+ * (written in weight_dtype).  x, dy, dx contiguous [rows, dim] in dtype. */
+int mt_rms_norm_bwd(const void* x, const void* weight, const float* rstd, const void* dy, void* dx, void* dweight,
+                    void* workspace, size_t workspace_bytes, int64_t rows, int dim, int dtype, int weight_dtype,
+                    void* stream);
+
+/* As mt_rms_norm_bwd on the stored new_residual, plus d_new_residual added to dx
+ * (dx is the gradient of both x and residual). */
+int mt_add_rms_norm_bwd(const void* new_residual, const void* weight, const float* rstd, const void* d_new_residual,
+                        const void* dy, void* dx, void* dweight, void* workspace, size_t workspace_bytes,
+                        int64_t rows, int dim, int dtype, int weight_dtype, void* stream);
+
+/* out = round(silu(gate)) * up, silu(g) = g / (1 + exp(-g)). */
+int mt_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/* dgate = round(dout * up) * sig * (1 + gate (1 - sig)), dup = dout * round(silu(gate)). */
+int mt_swiglu_bwd(const void* gate, const void* up, const void* dout, void* dgate, void* dup, int64_t n, int dtype,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MT_OPS_H_ */

@@ -1,4 +1,4 @@
-"""ctypes binding of libmt_attn.so (the C ABI declared in include/mt_attention.h).
+"""ctypes binding of libmt_attn.so (the C ABI declared in include/mt_attention.h and include/mt_ops.h).
 
 The library is loaded lazily on first use.  There is no fallback: if the
 library is missing the call raises, so a GPU run can never silently route
@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
+DTYPE_FP32 = 2
 
 # Every symbol the header declares; tests check the library exports them all.
 EXPORTS = (
@@ -27,6 +28,13 @@ EXPORTS = (
     "mt_gqa_attn_bwd_dq",
     "mt_gqa_attn_bwd_dkv",
     "mt_time_next_kernel",
+    "mt_rms_norm_fwd",
+    "mt_add_rms_norm_fwd",
+    "mt_rms_norm_bwd_workspace_size",
+    "mt_rms_norm_bwd",
+    "mt_add_rms_norm_bwd",
+    "mt_swiglu_fwd",
+    "mt_swiglu_bwd",
 )
 
 _lock = threading.Lock()
@@ -38,6 +46,16 @@ _F = ctypes.c_float
 _S = ctypes.c_size_t
 _FWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
 _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
+_L = ctypes.c_int64
+_OPS_SIGNATURES = {
+    "mt_rms_norm_fwd": (_I, [_P, _L, _P, _P, _P, _L, _I, _F, _I, _I, _P]),
+    "mt_add_rms_norm_fwd": (_I, [_P, _L, _P, _L, _P, _P, _P, _P, _L, _I, _F, _I, _I, _P]),
+    "mt_rms_norm_bwd_workspace_size": (_S, [_L, _I]),
+    "mt_rms_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
+    "mt_add_rms_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
+    "mt_swiglu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
+    "mt_swiglu_bwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _P]),
+}
 
 
 class HipAttentionError(RuntimeError):
@@ -76,6 +94,10 @@ def load() -> ctypes.CDLL:
             fn.argtypes = _BWD_ARGTYPES
         lib.mt_time_next_kernel.restype = _I
         lib.mt_time_next_kernel.argtypes = [_P, _P]
+        for name, (res, args) in _OPS_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
         _lib = lib
         return lib
 

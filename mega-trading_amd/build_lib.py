@@ -18,11 +18,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libmt_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["mt_attention.hip"]
+SOURCES = ["mt_attention.hip", "mt_ops.hip"]
 PROBE_NAME = "libmt_probe.so"
 PROBE_PATH = os.path.join(HERE, PROBE_NAME)
 PROBE_SOURCES = ["mfma_probe.hip"]
-HEADERS = ["mt_common.h", "attn_kernels.h"]
+HEADERS = ["mt_common.h", "attn_kernels.h", "lds_tile.h", "mt_abi.h", "ops_kernels.h"]
 ARCH = "gfx950"
 
 

@@ -13,12 +13,14 @@
 
 #include "../../include/mt_attention.h"
 #include "attn_kernels.h"
+#include "mt_abi.h"
+
+namespace mt_abi {
 
 namespace {
-
 thread_local char g_err[512] = "";
+}  // namespace
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -31,6 +33,28 @@ int ok() {
   g_err[0] = '\0';
   return MT_OK;
 }
+
+const char* last_error() { return g_err; }
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+}  // namespace mt_abi
+
+namespace {
+
+using mt_abi::device_cus;
+using mt_abi::fail;
+using mt_abi::ok;
 
 // Events armed by mt_time_next_kernel(): attached to the next main kernel
 // launch made by this thread (hipExtLaunchKernel stamps them with that
@@ -67,18 +91,6 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, const float* c
   if (cs && (reinterpret_cast<uintptr_t>(cs) % 16 || reinterpret_cast<uintptr_t>(sn) % 16))
     return fail(MT_E_ROPE, "RoPE tables must be 16-byte aligned");
   return MT_OK;
-}
-
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
 }
 
 int kv_keys(int) { return mt::kKvKeys; }
@@ -252,7 +264,7 @@ extern "C" {
 
 int mt_version(void) { return (0 << 16) | 3; }
 
-const char* mt_last_error(void) { return g_err; }
+const char* mt_last_error(void) { return mt_abi::last_error(); }
 
 int mt_time_next_kernel(void* start_event, void* stop_event) {
   if ((start_event == nullptr) != (stop_event == nullptr))

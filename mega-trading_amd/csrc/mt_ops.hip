@@ -1,0 +1,255 @@
+// C ABI of the decoder operators (RMSNorm, residual-add + RMSNorm, SwiGLU
+// gate): argument checks, launch geometry and dispatch to ops_kernels.h.
+// Declared in include/mt_ops.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/mt_ops.h"
+#include "mt_abi.h"
+#include "ops_kernels.h"
+
+namespace {
+
+using mt_abi::device_cus;
+using mt_abi::fail;
+using mt_abi::ok;
+namespace K = mt::ops;
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int check_dtype(int dtype, int weight_dtype) {
+  if (dtype != MT_DTYPE_BF16 && dtype != MT_DTYPE_FP16 && dtype != MT_DTYPE_FP32)
+    return fail(MT_E_DTYPE, "dtype code %d unsupported", dtype);
+  if (weight_dtype != dtype && weight_dtype != MT_DTYPE_FP32)
+    return fail(MT_E_DTYPE, "weight dtype code %d must equal the tensor dtype (%d) or be fp32", weight_dtype, dtype);
+  return MT_OK;
+}
+
+int check_rows(int64_t rows, int dim) {
+  if (rows < 0 || rows > (int64_t(1) << 32))
+    return fail(MT_E_SHAPE, "rows must be in [0, 2^32] (got %lld)", (long long)rows);
+  if (dim < 8 || dim > 4096 || dim % 8)
+    return fail(MT_E_SHAPE, "dim %d unsupported (a multiple of 8 in [8, 4096])", dim);
+  return MT_OK;
+}
+
+int check_ptr(const char* name, const void* p) {
+  if (!p) return fail(MT_E_NULL, "%s is NULL", name);
+  if (!aligned16(p)) return fail(MT_E_STRIDE, "%s must be 16-byte aligned", name);
+  return MT_OK;
+}
+
+int check_stride(const char* name, int64_t stride, int dim) {
+  if (stride < dim || stride % 8) return fail(MT_E_STRIDE, "%s row stride %lld must be >= dim and a multiple of 8",
+                                               name, (long long)stride);
+  return MT_OK;
+}
+
+// chunks of 8 values per lane that hold a row of dim values: 1, 2, 4 or 8
+int chunks(int dim) {
+  const int nch = (dim / 8 + 63) / 64;
+  return nch <= 1 ? 1 : nch <= 2 ? 2 : nch <= 4 ? 4 : 8;
+}
+
+// workgroups of the RMSNorm backward: 4 per CU (16 waves), each striding over rows
+int bwd_blocks(int64_t rows) {
+  const int64_t want = (rows + 3) / 4;
+  const int64_t cap = 4L * device_cus();
+  return (int)(want < 1 ? 1 : want < cap ? want : cap);
+}
+
+// ---- dispatch over (dtype, weight dtype, chunks) ---------------------------
+template <int DT, int WT, int NCH, bool ADD>
+hipError_t fwd_launch(const void* x, int64_t sx, const void* r, int64_t sr, const void* w, void* nr, void* y, float* rstd,
+                      int64_t rows, int dim, float eps, hipStream_t st) {
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  hipLaunchKernelGGL((K::rmsnorm_fwd_kernel<DT, WT, NCH, ADD>), grid, dim3(256), 0, st, x, sx, r, sr, w, nr, y, rstd,
+                     rows, dim, eps);
+  return hipGetLastError();
+}
+
+template <int DT, int WT, int NCH, bool ADD>
+hipError_t bwd_launch(const void* s, const void* w, const float* rstd, const void* dy, const void* dres, void* ds,
+                      void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
+  const int nb = bwd_blocks(rows);
+  if (rows > 0) {
+    hipLaunchKernelGGL((K::rmsnorm_bwd_kernel<DT, WT, NCH, ADD>), dim3(nb), dim3(256), 0, st, s, w, rstd, dy, dres, ds,
+                       partial, rows, dim);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((K::column_sum_kernel<WT>), dim3((dim + 63) / 64), dim3(256), 0, st, partial,
+                     rows > 0 ? nb : 0, dim, dw);
+  return hipGetLastError();
+}
+
+template <int DT, int WT, bool ADD>
+hipError_t fwd_nch(int nch, const void* x, int64_t sx, const void* r, int64_t sr, const void* w, void* nr, void* y,
+                   float* rstd, int64_t rows, int dim, float eps, hipStream_t st) {
+  switch (nch) {
+    case 1: return fwd_launch<DT, WT, 1, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    case 2: return fwd_launch<DT, WT, 2, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    case 4: return fwd_launch<DT, WT, 4, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    default: return fwd_launch<DT, WT, 8, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+  }
+}
+
+template <int DT, int WT, bool ADD>
+hipError_t bwd_nch(int nch, const void* s, const void* w, const float* rstd, const void* dy, const void* dres, void* ds,
+                   void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
+  switch (nch) {
+    case 1: return bwd_launch<DT, WT, 1, ADD>(s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+    case 2: return bwd_launch<DT, WT, 2, ADD>(s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+    case 4: return bwd_launch<DT, WT, 4, ADD>(s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+    default: return bwd_launch<DT, WT, 8, ADD>(s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+  }
+}
+
+template <bool ADD>
+hipError_t fwd_dispatch(int dtype, int wdt, const void* x, int64_t sx, const void* r, int64_t sr, const void* w,
+                        void* nr, void* y, float* rstd, int64_t rows, int dim, float eps, hipStream_t st) {
+  const int n = chunks(dim);
+  if (dtype == MT_DTYPE_FP32) return fwd_nch<K::kDtFP32, K::kDtFP32, ADD>(n, x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+  if (dtype == MT_DTYPE_BF16) {
+    if (wdt == MT_DTYPE_FP32) return fwd_nch<K::kDtBF16, K::kDtFP32, ADD>(n, x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    return fwd_nch<K::kDtBF16, K::kDtBF16, ADD>(n, x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+  }
+  if (wdt == MT_DTYPE_FP32) return fwd_nch<K::kDtFP16, K::kDtFP32, ADD>(n, x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+  return fwd_nch<K::kDtFP16, K::kDtFP16, ADD>(n, x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+}
+
+template <bool ADD>
+hipError_t bwd_dispatch(int dtype, int wdt, const void* s, const void* w, const float* rstd, const void* dy,
+                        const void* dres, void* ds, void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
+  const int n = chunks(dim);
+  if (dtype == MT_DTYPE_FP32) return bwd_nch<K::kDtFP32, K::kDtFP32, ADD>(n, s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+  if (dtype == MT_DTYPE_BF16) {
+    if (wdt == MT_DTYPE_FP32) return bwd_nch<K::kDtBF16, K::kDtFP32, ADD>(n, s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+    return bwd_nch<K::kDtBF16, K::kDtBF16, ADD>(n, s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+  }
+  if (wdt == MT_DTYPE_FP32) return bwd_nch<K::kDtFP16, K::kDtFP32, ADD>(n, s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+  return bwd_nch<K::kDtFP16, K::kDtFP16, ADD>(n, s, w, rstd, dy, dres, ds, dw, partial, rows, dim, st);
+}
+
+int swiglu_blocks(int64_t n) {
+  const int64_t nvec = n / 8;
+  const int64_t want = (nvec + 255) / 256;
+  const int64_t cap = 8L * device_cus();
+  return (int)(want < 1 ? 1 : want < cap ? want : cap);
+}
+
+int rms_bwd_common(const void* s, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* ws,
+                   size_t ws_bytes, int64_t rows, int dim, int dtype, int wdt) {
+  int rc;
+  if ((rc = check_dtype(dtype, wdt)) || (rc = check_rows(rows, dim))) return rc;
+  if ((rc = check_ptr("weight", w)) || (rc = check_ptr("dweight", dw)) || (rc = check_ptr("workspace", ws))) return rc;
+  if (rows > 0) {
+    if ((rc = check_ptr("x", s)) || (rc = check_ptr("dy", dy)) || (rc = check_ptr("dx", dx))) return rc;
+    if (!rstd) return fail(MT_E_NULL, "rstd is NULL");
+  }
+  if (ws_bytes < mt_rms_norm_bwd_workspace_size(rows, dim))
+    return fail(MT_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", ws_bytes,
+                mt_rms_norm_bwd_workspace_size(rows, dim));
+  return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_rms_norm_fwd(const void* x, int64_t x_row_stride, const void* weight, void* y, float* rstd, int64_t rows,
+                    int dim, float eps, int dtype, int weight_dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, weight_dtype)) || (rc = check_rows(rows, dim))) return rc;
+  if ((rc = check_ptr("weight", weight))) return rc;
+  if (rows == 0) return ok();
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("y", y)) || (rc = check_stride("x", x_row_stride, dim))) return rc;
+  if (!rstd) return fail(MT_E_NULL, "rstd is NULL");
+  const hipError_t e = fwd_dispatch<false>(dtype, weight_dtype, x, x_row_stride, nullptr, 0, weight, nullptr, y, rstd,
+                                           rows, dim, eps, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_add_rms_norm_fwd(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                        const void* weight, void* new_residual, void* y, float* rstd, int64_t rows, int dim,
+                        float eps, int dtype, int weight_dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, weight_dtype)) || (rc = check_rows(rows, dim))) return rc;
+  if ((rc = check_ptr("weight", weight))) return rc;
+  if (rows == 0) return ok();
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("residual", residual)) || (rc = check_ptr("new_residual", new_residual)) ||
+      (rc = check_ptr("y", y)) || (rc = check_stride("x", x_row_stride, dim)) ||
+      (rc = check_stride("residual", residual_row_stride, dim)))
+    return rc;
+  if (!rstd) return fail(MT_E_NULL, "rstd is NULL");
+  const hipError_t e = fwd_dispatch<true>(dtype, weight_dtype, x, x_row_stride, residual, residual_row_stride, weight,
+                                          new_residual, y, rstd, rows, dim, eps, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+size_t mt_rms_norm_bwd_workspace_size(int64_t rows, int dim) {
+  if (rows < 0 || dim < 0) return 0;
+  return ((size_t)bwd_blocks(rows) * (size_t)dim * sizeof(float) + 255) / 256 * 256;
+}
+
+int mt_rms_norm_bwd(const void* x, const void* weight, const float* rstd, const void* dy, void* dx, void* dweight,
+                    void* workspace, size_t workspace_bytes, int64_t rows, int dim, int dtype, int weight_dtype,
+                    void* stream) {
+  const int rc = rms_bwd_common(x, weight, rstd, dy, dx, dweight, workspace, workspace_bytes, rows, dim, dtype,
+                                weight_dtype);
+  if (rc) return rc;
+  const hipError_t e = bwd_dispatch<false>(dtype, weight_dtype, x, weight, rstd, dy, nullptr, dx, dweight,
+                                           static_cast<float*>(workspace), rows, dim, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_add_rms_norm_bwd(const void* new_residual, const void* weight, const float* rstd, const void* d_new_residual,
+                        const void* dy, void* dx, void* dweight, void* workspace, size_t workspace_bytes,
+                        int64_t rows, int dim, int dtype, int weight_dtype, void* stream) {
+  int rc = rms_bwd_common(new_residual, weight, rstd, dy, dx, dweight, workspace, workspace_bytes, rows, dim, dtype,
+                          weight_dtype);
+  if (rc) return rc;
+  if (rows > 0 && (rc = check_ptr("d_new_residual", d_new_residual))) return rc;
+  const hipError_t e = bwd_dispatch<true>(dtype, weight_dtype, new_residual, weight, rstd, dy, d_new_residual, dx,
+                                          dweight, static_cast<float*>(workspace), rows, dim, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, dtype))) return rc;
+  if (n < 0) return fail(MT_E_SHAPE, "n must be >= 0 (got %lld)", (long long)n);
+  if (n == 0) return ok();
+  if ((rc = check_ptr("gate", gate)) || (rc = check_ptr("up", up)) || (rc = check_ptr("out", out))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(swiglu_blocks(n));
+  if (dtype == MT_DTYPE_BF16) hipLaunchKernelGGL((K::swiglu_fwd_kernel<K::kDtBF16>), grid, dim3(256), 0, st, gate, up, out, n);
+  else if (dtype == MT_DTYPE_FP16) hipLaunchKernelGGL((K::swiglu_fwd_kernel<K::kDtFP16>), grid, dim3(256), 0, st, gate, up, out, n);
+  else hipLaunchKernelGGL((K::swiglu_fwd_kernel<K::kDtFP32>), grid, dim3(256), 0, st, gate, up, out, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_swiglu_bwd(const void* gate, const void* up, const void* dout, void* dgate, void* dup, int64_t n, int dtype,
+                  void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, dtype))) return rc;
+  if (n < 0) return fail(MT_E_SHAPE, "n must be >= 0 (got %lld)", (long long)n);
+  if (n == 0) return ok();
+  if ((rc = check_ptr("gate", gate)) || (rc = check_ptr("up", up)) || (rc = check_ptr("dout", dout)) ||
+      (rc = check_ptr("dgate", dgate)) || (rc = check_ptr("dup", dup)))
+    return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(swiglu_blocks(n));
+  if (dtype == MT_DTYPE_BF16)
+    hipLaunchKernelGGL((K::swiglu_bwd_kernel<K::kDtBF16>), grid, dim3(256), 0, st, gate, up, dout, dgate, dup, n);
+  else if (dtype == MT_DTYPE_FP16)
+    hipLaunchKernelGGL((K::swiglu_bwd_kernel<K::kDtFP16>), grid, dim3(256), 0, st, gate, up, dout, dgate, dup, n);
+  else
+    hipLaunchKernelGGL((K::swiglu_bwd_kernel<K::kDtFP32>), grid, dim3(256), 0, st, gate, up, dout, dgate, dup, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+}  // extern "C"

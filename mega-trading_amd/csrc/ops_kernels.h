@@ -1,0 +1,341 @@
+// gfx950 kernels for the decoder's memory-bound operators around the
+// attention: RMSNorm (optionally fused with the residual add) and the SwiGLU
+// gate, forward and backward.
+//
+// Reference operators (src/mega_trading/kernels/triton_ops.py):
+//   RMSNorm          :11-15, :133-184, kernels :528-539 (forward), :633-666 (backward)
+//   add + RMSNorm    :18-42, :217-291, kernels :541-566, :569-608
+//   SwiGLU gate      :57-61, :431-474, kernels :774-782, :799-819
+//
+// All of them move each byte once: one wave owns one row (RMSNorm, rows of D
+// <= 4096 values held in registers as 8-value chunks), the SwiGLU gate streams
+// 8 values per lane per step.  Arithmetic is fp32; storage is bf16, fp16 or
+// fp32 (tensor dtype codes as in include/mt_ops.h).  The roundings the
+// reference performs between steps are reproduced (e.g. silu(g) is rounded to
+// the storage type before it multiplies `up`), so 16-bit results match the
+// reference's to the last bit up to the last-ulp differences of exp.
+#pragma once
+
+#include <type_traits>
+
+#include "mt_common.h"
+
+namespace mt {
+namespace ops {
+
+constexpr int kDtBF16 = 0;
+constexpr int kDtFP16 = 1;
+constexpr int kDtFP32 = 2;
+
+// ---------------------------------------------------------------------------
+// storage <-> fp32, 8 consecutive values at a time (16 bytes for 16-bit types,
+// 32 bytes for fp32); element offsets must be multiples of 8
+// ---------------------------------------------------------------------------
+template <int DT>
+struct IO {
+  static __device__ __forceinline__ void load8(const void* base, int64_t i, float* v) {
+    if constexpr (DT == kDtFP32) {
+      const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
+      const f32x4 a = p[0], b = p[1];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = a[k];
+        v[4 + k] = b[k];
+      }
+    } else {
+      using E = typename std::conditional<DT == kDtBF16, BF16, FP16>::type;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[2 * k] = lo_f<E>(w[k]);
+        v[2 * k + 1] = hi_f<E>(w[k]);
+      }
+    }
+  }
+  static __device__ __forceinline__ void store8(void* base, int64_t i, const float* v) {
+    if constexpr (DT == kDtFP32) {
+      f32x4* p = reinterpret_cast<f32x4*>(static_cast<float*>(base) + i);
+      p[0] = f32x4{v[0], v[1], v[2], v[3]};
+      p[1] = f32x4{v[4], v[5], v[6], v[7]};
+    } else {
+      using E = typename std::conditional<DT == kDtBF16, BF16, FP16>::type;
+      u32x4 w;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = pack2<E>(v[2 * k], v[2 * k + 1]);
+      *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = w;
+    }
+  }
+  static __device__ __forceinline__ float load1(const void* base, int64_t i) {
+    if constexpr (DT == kDtFP32) return static_cast<const float*>(base)[i];
+    else if constexpr (DT == kDtBF16) return BF16::to_f(static_cast<const uint16_t*>(base)[i]);
+    else return FP16::to_f(static_cast<const uint16_t*>(base)[i]);
+  }
+  static __device__ __forceinline__ void store1(void* base, int64_t i, float x) {
+    if constexpr (DT == kDtFP32) static_cast<float*>(base)[i] = x;
+    else if constexpr (DT == kDtBF16) static_cast<uint16_t*>(base)[i] = uint16_t(pack2<BF16>(x, 0.f) & 0xffffu);
+    else static_cast<uint16_t*>(base)[i] = uint16_t(pack2<FP16>(x, 0.f) & 0xffffu);
+  }
+  // the value x takes after a store to and a load from this storage type
+  static __device__ __forceinline__ float round(float x) {
+    if constexpr (DT == kDtFP32) return x;
+    else if constexpr (DT == kDtBF16) return lo_f<BF16>(pack2<BF16>(x, 0.f));
+    else return lo_f<FP16>(pack2<FP16>(x, 0.f));
+  }
+};
+
+// Sum over the 64 lanes of a wave; every lane gets the same, bit-identical
+// value (each butterfly level adds the same two operands on both partners).
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// ===========================================================================
+// RMSNorm forward (ADD: the residual add fused in front)
+//   ADD:  s = x + r (fp32), new_res = s (stored in DT), y = s * rstd * w
+//   else: y = x * rstd * w
+//   rstd = 1 / sqrt(mean(s^2) + eps) (fp32, one per row)
+// One wave per row; lane L holds chunks L, L + 64, ... (8 values each).
+// ===========================================================================
+template <int DT, int WT, int NCH, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const void* x, int64_t sx, const void* res, int64_t sr,
+                                                          const void* w, void* new_res, void* y, float* rstd,
+                                                          int64_t rows, int D, float eps) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const int nch = D >> 3;
+  float v[NCH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = lane + 64 * k;
+    if (c < nch) {
+      IO<DT>::load8(x, row * sx + 8 * c, v[k]);
+      if constexpr (ADD) {
+        float r[8];
+        IO<DT>::load8(res, row * sr + 8 * c, r);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[k][j] += r[j];
+        IO<DT>::store8(new_res, row * D + 8 * c, v[k]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[k][j] * v[k][j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = __builtin_amdgcn_rsqf(ss / float(D) + eps);
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = lane + 64 * k;
+    if (c < nch) {
+      float wv[8], o[8];
+      IO<WT>::load8(w, 8 * c, wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = v[k][j] * inv * wv[j];
+      IO<DT>::store8(y, row * D + 8 * c, o);
+    }
+  }
+  if (lane == 0) rstd[row] = inv;
+}
+
+// ===========================================================================
+// RMSNorm backward (dy and ds in the storage type of s).  With g = dy * w
+// (fp32) and c = sum(g * s) over the row:
+//   ds = rstd * (g - s * rstd^2 / D * c)        (+ d_new_res when ADD)
+//   dw = sum over rows of dy * s * rstd         (per-workgroup partial sums)
+// s is x (or the stored new residual when ADD).  Waves stride over rows; each
+// lane accumulates its dw chunks in registers, the 4 waves of a workgroup
+// combine them in LDS and write one fp32 partial row per workgroup.
+// ===========================================================================
+template <int DT, int WT, int NCH, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const void* s, const void* w, const float* rstd,
+                                                          const void* dy, const void* dres, void* ds,
+                                                          float* partial, int64_t rows, int D) {
+  __shared__ float red[3][NCH * 512];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nch = D >> 3;
+  const float inv_d = 1.f / float(D);
+  float wv[NCH][8], acc[NCH][8];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = lane + 64 * k;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[k][j] = 0.f;
+    if (c < nch) IO<WT>::load8(w, 8 * c, wv[k]);
+  }
+  // U rows per iteration, all loads issued before any arithmetic, so each wave
+  // keeps U rows of traffic in flight
+  constexpr int U = NCH <= 2 ? 2 : 1;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t row0 = (int64_t)blockIdx.x * 4 + wave; row0 < rows; row0 += U * waves) {
+    float sv[U][NCH][8], g[U][NCH][8], r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = row0 + u * waves;
+      if (row < rows) {
+        r[u] = rstd[row];
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+          const int c = lane + 64 * k;
+          if (c < nch) {
+            IO<DT>::load8(s, row * D + 8 * c, sv[u][k]);
+            IO<DT>::load8(dy, row * D + 8 * c, g[u][k]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = row0 + u * waves;
+      if (row >= rows) break;
+      float cs = 0.f;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int c = lane + 64 * k;
+        if (c < nch) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            acc[k][j] += g[u][k][j] * sv[u][k][j] * r[u];
+            g[u][k][j] *= wv[k][j];
+            cs += g[u][k][j] * sv[u][k][j];
+          }
+        }
+      }
+      cs = wave_sum(cs);
+      const float f = r[u] * r[u] * inv_d * cs;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int c = lane + 64 * k;
+        if (c < nch) {
+          float o[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) o[j] = r[u] * (g[u][k][j] - sv[u][k][j] * f);
+          if constexpr (ADD) {
+            float dr[8];
+            IO<DT>::load8(dres, row * D + 8 * c, dr);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] += dr[j];
+          }
+          IO<DT>::store8(ds, row * D + 8 * c, o);
+        }
+      }
+    }
+  }
+  // workgroup reduction of dw: waves 1..3 park their sums, wave 0 adds them
+  if (wave > 0) {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[wave - 1][(lane + 64 * k) * 8 + j] = acc[k][j];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      const int c = lane + 64 * k;
+      if (c < nch) {
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          o[j] = acc[k][j] + red[0][c * 8 + j] + red[1][c * 8 + j] + red[2][c * 8 + j];
+        IO<kDtFP32>::store8(partial, (int64_t)blockIdx.x * D + 8 * c, o);
+      }
+    }
+  }
+}
+
+// dw[d] = sum over nb partial rows, stored as WT.  A block owns 64 columns;
+// wave q sums rows q, q + 4, ... into 8 independent accumulators (8 loads in
+// flight per lane), then wave 0 adds the four quarter sums.  The order of every
+// addition is fixed, so the result is deterministic.
+template <int WT>
+__global__ __launch_bounds__(256) void column_sum_kernel(const float* partial, int nb, int D, void* out) {
+  __shared__ float quarter[4][64];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int d = blockIdx.x * 64 + lane;
+  float acc = 0.f;
+  if (d < D) {
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int b = wave;
+    for (; b + 28 < nb; b += 32) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a[k] += partial[(int64_t)(b + 4 * k) * D + d];
+    }
+    for (; b < nb; b += 4) a[0] += partial[(int64_t)b * D + d];
+    acc = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+  }
+  quarter[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && d < D) IO<WT>::store1(out, d, ((quarter[0][lane] + quarter[1][lane]) + quarter[2][lane]) + quarter[3][lane]);
+}
+
+// ===========================================================================
+// SwiGLU gate: out = silu(g) * u, silu(g) = g / (1 + exp(-g)) in fp32.
+// Forward rounds silu(g) to the storage type before the product
+// (triton_ops.py:781: silu.to(up.dtype) * up).  Backward
+// (triton_ops.py:814-819):
+//   t  = dy * u                 rounded to the storage type
+//   dg = (t * sig) * (1 + g (1 - sig)),  sig = 1 / (1 + exp(-g))
+//   du = dy * round(silu(g))
+// with silu(g) evaluated as in the forward, so du uses exactly the rounded
+// forward activation.
+// Flat over n values; lanes take 8 consecutive values, the last n % 8 values
+// are handled one per lane.
+// ===========================================================================
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_fwd_kernel(const void* gate, const void* up, void* out, int64_t n) {
+  const int64_t nvec = n >> 3;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride) {
+    float g[8], u[8], o[8];
+    IO<DT>::load8(gate, 8 * i, g);
+    IO<DT>::load8(up, 8 * i, u);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[j] / (1.f + expf(-g[j]))) * u[j];
+    IO<DT>::store8(out, 8 * i, o);
+  }
+  const int64_t t = 8 * nvec + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t < n && (int64_t)blockIdx.x * 256 + threadIdx.x < 8) {
+    const float g = IO<DT>::load1(gate, t);
+    IO<DT>::store1(out, t, IO<DT>::round(g / (1.f + expf(-g))) * IO<DT>::load1(up, t));
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const void* up, const void* dout,
+                                                         void* dgate, void* dup, int64_t n) {
+  const int64_t nvec = n >> 3;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride) {
+    float g[8], u[8], dy[8], dg[8], du[8];
+    IO<DT>::load8(gate, 8 * i, g);
+    IO<DT>::load8(up, 8 * i, u);
+    IO<DT>::load8(dout, 8 * i, dy);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = expf(-g[j]);
+      const float sg = 1.f / (1.f + e);
+      const float t = IO<DT>::round(dy[j] * u[j]);
+      dg[j] = (t * sg) * (1.f + g[j] * (1.f - sg));
+      du[j] = dy[j] * IO<DT>::round(g[j] / (1.f + e));
+    }
+    IO<DT>::store8(dgate, 8 * i, dg);
+    IO<DT>::store8(dup, 8 * i, du);
+  }
+  const int64_t t = 8 * nvec + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t < n && (int64_t)blockIdx.x * 256 + threadIdx.x < 8) {
+    const float g = IO<DT>::load1(gate, t), u = IO<DT>::load1(up, t), dy = IO<DT>::load1(dout, t);
+    const float e = expf(-g);
+    const float sg = 1.f / (1.f + e);
+    IO<DT>::store1(dgate, t, (IO<DT>::round(dy * u) * sg) * (1.f + g * (1.f - sg)));
+    IO<DT>::store1(dup, t, dy * IO<DT>::round(g / (1.f + e)));
+  }
+}
+
+}  // namespace ops
+}  // namespace mt

@@ -16,8 +16,13 @@ The module tree, argument names and routing follow the reference model
   ``fuse_rope=False`` keeps the reference's two calls, ``self.rope`` then
   ``attention(query, key, value, repeats=...)`` (``model.py:223,226``).
 
-Only the attention is a HIP kernel here; RMSNorm, SwiGLU and the loss use
-torch ops (the reference's Triton versions of those are separate operators).
+The other operators follow the reference's routing too: the SwiGLU gate
+takes the attention backend (``model.py:179-183, 252-253``), so "triton" /
+"hip" use the HIP gate (``ops.swiglu_gate``); the reference builds its RMSNorm
+modules without a backend (``model.py:166, 176``, torch ``F.rms_norm``), which
+"triton" keeps, while "hip" -- this package's own value -- also runs them on
+the HIP RMSNorm kernels (``ops.rms_norm``).  The loss head is torch
+``F.cross_entropy``.
 """
 
 from __future__ import annotations
@@ -30,6 +35,8 @@ from torch import nn
 
 from .attention import attention as _hip_attention
 from .attention import rope_attention as _hip_rope_attention
+from .ops import rms_norm as _hip_rms_norm
+from .ops import swiglu_gate as _hip_swiglu_gate
 
 __all__ = ["TradingModel", "LlamaDecoderBlock", "LlamaAttention", "SwiGLU", "RMSNorm", "RotaryEmbedding",
            "ATTENTION_BACKENDS", "HIP_BACKENDS"]
@@ -86,7 +93,7 @@ class TradingModel(nn.Module):
                 for _ in range(layers)
             ]
         )
-        self.norm = RMSNorm(hidden_dim, eps=norm_eps)
+        self.norm = RMSNorm(hidden_dim, eps=norm_eps, operator_backend=_norm_backend(attention_backend))
         self.output = nn.Linear(hidden_dim, vocab_size, bias=False)
         self.apply(_init_weights)
         self.output.weight = self.token_embedding.weight  # tied after init, as model.py:71
@@ -137,7 +144,8 @@ class LlamaDecoderBlock(nn.Module):
         fuse_rope: bool = True,
     ) -> None:
         super().__init__()
-        self.attention_norm = RMSNorm(hidden_dim, eps=norm_eps)
+        norm_backend = _norm_backend(attention_backend)
+        self.attention_norm = RMSNorm(hidden_dim, eps=norm_eps, operator_backend=norm_backend)
         self.attention = LlamaAttention(
             hidden_dim=hidden_dim,
             block_size=block_size,
@@ -148,8 +156,9 @@ class LlamaDecoderBlock(nn.Module):
             attention_backend=attention_backend,
             fuse_rope=fuse_rope,
         )
-        self.ffn_norm = RMSNorm(hidden_dim, eps=norm_eps)
-        self.feed_forward = SwiGLU(hidden_dim, intermediate_dim or _llama_intermediate_dim(hidden_dim), dropout)
+        self.ffn_norm = RMSNorm(hidden_dim, eps=norm_eps, operator_backend=norm_backend)
+        self.feed_forward = SwiGLU(hidden_dim, intermediate_dim or _llama_intermediate_dim(hidden_dim), dropout,
+                                   operator_backend=attention_backend)
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         hidden = hidden + self.attention(self.attention_norm(hidden))
@@ -210,29 +219,44 @@ class LlamaAttention(nn.Module):
 
 
 class SwiGLU(nn.Module):
-    """w2(silu(w1 x) * w3 x) (``model.py:240-256``)."""
+    """w2(silu(w1 x) * w3 x) (``model.py:240-256``); the gate on HIP for "triton" / "hip"."""
 
-    def __init__(self, hidden_dim: int, intermediate_dim: int, dropout: float) -> None:
+    def __init__(self, hidden_dim: int, intermediate_dim: int, dropout: float, operator_backend: str = "auto") -> None:
         super().__init__()
         self.w1 = nn.Linear(hidden_dim, intermediate_dim, bias=False)
         self.w2 = nn.Linear(intermediate_dim, hidden_dim, bias=False)
         self.w3 = nn.Linear(hidden_dim, intermediate_dim, bias=False)
         self.dropout = nn.Dropout(dropout)
+        self.operator_backend = operator_backend
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
-        return self.w2(self.dropout(F.silu(self.w1(hidden)) * self.w3(hidden)))
+        gate = self.w1(hidden)
+        up = self.w3(hidden)
+        if self.operator_backend in HIP_BACKENDS:
+            gated = _hip_swiglu_gate(gate, up)
+        else:
+            gated = F.silu(gate) * up
+        return self.w2(self.dropout(gated))
 
 
 class RMSNorm(nn.Module):
-    """``F.rms_norm`` with a learned scale (``model.py:259-269``)."""
+    """``F.rms_norm`` with a learned scale (``model.py:259-269``); HIP kernels for "hip"."""
 
-    def __init__(self, hidden_dim: int, eps: float = 1e-5) -> None:
+    def __init__(self, hidden_dim: int, eps: float = 1e-5, operator_backend: str = "auto") -> None:
         super().__init__()
         self.weight = nn.Parameter(torch.ones(hidden_dim))
         self.eps = eps
+        self.operator_backend = operator_backend
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        if self.operator_backend == "hip":
+            return _hip_rms_norm(hidden, self.weight, eps=self.eps)
         return F.rms_norm(hidden, (hidden.shape[-1],), self.weight, eps=self.eps)
+
+
+def _norm_backend(attention_backend: str) -> str:
+    """The reference builds its norms without a backend (torch); "hip" moves them to HIP."""
+    return "hip" if attention_backend == "hip" else "auto"
 
 
 class RotaryEmbedding(nn.Module):

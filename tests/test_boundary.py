@@ -16,11 +16,11 @@ import torch
 from torch._subclasses.fake_tensor import FakeTensorMode
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "mt_attention.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("mt_attention.h", "mt_ops.h")]
 
 
 def _header_functions() -> list[str]:
-    text = open(HEADER).read()
+    text = "\n".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mt_\w+)\s*\(", text, flags=re.M)))
 
 
@@ -55,6 +55,41 @@ def _fwd_call(lib, q=0x1000, k=0x1000, v=0x1000, o=0x1000, lse=0x1000, b=1, hq=4
         strides = [hq * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hkv * t * d, t * d, d, 1, hq * t * d, t * d, d, 1]
     arr = (ctypes.c_int64 * 16)(*strides)
     return lib.mt_gqa_attn_fwd(q, k, v, o, lse, qrot, krot, b, hq, hkv, t, d, arr, 0.125, dtype, cos, sin, None)
+
+
+def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
+    lib = mta._native.load()
+    p = 0x10000  # aligned, never dereferenced: every call below fails validation first
+    BF16, FP32 = mta._native.DTYPE_BF16, mta._native.DTYPE_FP32
+    assert lib.mt_rms_norm_fwd(p, 16, p, p, p, 4, 12, 1e-5, FP32, FP32, None) == -2  # dim not a multiple of 8
+    assert b"dim 12" in lib.mt_last_error()
+    assert lib.mt_rms_norm_fwd(p, 8192, p, p, p, 4, 8192, 1e-5, FP32, FP32, None) == -2  # dim > 4096
+    assert lib.mt_rms_norm_fwd(p, 16, p, p, p, 4, 16, 1e-5, 7, FP32, None) == -4
+    assert lib.mt_rms_norm_fwd(p, 16, p, p, p, 4, 16, 1e-5, BF16, mta._native.DTYPE_FP16, None) == -4
+    assert lib.mt_rms_norm_fwd(p + 2, 16, p, p, p, 4, 16, 1e-5, FP32, FP32, None) == -3  # misaligned x
+    assert lib.mt_rms_norm_fwd(p, 12, p, p, p, 4, 16, 1e-5, FP32, FP32, None) == -3  # row stride < dim
+    assert lib.mt_rms_norm_fwd(p, 16, None, p, p, 4, 16, 1e-5, FP32, FP32, None) == -1
+    assert lib.mt_rms_norm_fwd(p, 16, p, p, p, 0, 16, 1e-5, FP32, FP32, None) == 0  # zero rows: nothing to do
+    need = lib.mt_rms_norm_bwd_workspace_size(1000, 512)
+    assert need >= 512 * 4 and need % 256 == 0
+    assert lib.mt_rms_norm_bwd(p, p, p, p, p, p, p, need - 1, 1000, 512, FP32, FP32, None) == -6
+    assert b"workspace" in lib.mt_last_error()
+    assert lib.mt_add_rms_norm_fwd(p, 16, p, 8, p, p, p, p, 4, 16, 1e-5, FP32, FP32, None) == -3  # residual stride
+    assert lib.mt_swiglu_fwd(p, p, p, -1, BF16, None) == -2
+    assert lib.mt_swiglu_fwd(p, p + 8, p, 100, BF16, None) == -3
+    assert lib.mt_swiglu_bwd(p, p, None, p, p, 100, BF16, None) == -1
+    assert lib.mt_swiglu_fwd(None, None, None, 0, BF16, None) == 0  # n = 0: nothing to do
+    assert lib.mt_last_error() == b""
+
+
+def test_ops_reject_cpu_tensors(mta):
+    x = torch.zeros(4, 16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mta.rms_norm(x, torch.ones(16), eps=1e-5)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mta.add_rms_norm(x, x, torch.ones(16), eps=1e-5)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mta.swiglu_gate(x, x)
 
 
 def test_kernel_timer_arming(mta):

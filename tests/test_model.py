@@ -11,6 +11,7 @@ from unittest.mock import patch
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 model_mod = importlib.import_module("mega-trading_amd.model")
 workload = importlib.import_module("mega-trading_amd.workload")
@@ -147,3 +148,25 @@ def test_zipf_batch_is_seeded_shifted_and_heavy_headed():
     p1 = 1.0 / sum(k ** -1.1 for k in range(1, 16385))
     assert abs(counts[0] / x.numel() - p1) < 0.03  # rank 1 carries ~10% of the mass
     assert counts[0] > counts[1] > counts[10]
+
+
+@pytest.mark.parametrize("backend,gate_hip,norm_hip", [("auto", False, False), ("triton", True, False), ("hip", True, True)])
+def test_operator_routing_follows_the_reference(backend, gate_hip, norm_hip):
+    # SwiGLU takes the attention backend (reference model.py:179-183); the reference's
+    # norms have none (model.py:166,176), so only this package's "hip" value moves them
+    m = model_mod.TradingModel(vocab_size=32, block_size=8, hidden_dim=16, layers=1, attention_heads=4, kv_heads=2,
+                               dropout=0.0, rope_theta=10_000.0, attention_backend=backend)
+    assert m.blocks[0].feed_forward.operator_backend == backend
+    assert m.blocks[0].attention_norm.operator_backend == ("hip" if norm_hip else "auto")
+    assert m.norm.operator_backend == m.blocks[0].ffn_norm.operator_backend
+    hidden = torch.randn(1, 8, 16)
+    ffn = m.blocks[0].feed_forward
+    with patch("mega-trading_amd.model._hip_swiglu_gate", side_effect=lambda g, u: F.silu(g) * u) as gate:
+        ffn(hidden)
+    assert gate.called == gate_hip
+    norm = m.blocks[0].attention_norm
+    with patch("mega-trading_amd.model._hip_rms_norm", side_effect=lambda x, w, eps: x) as rms:
+        norm(hidden)
+    assert rms.called == norm_hip
+    if norm_hip:
+        assert rms.call_args.kwargs["eps"] == 1e-5 and rms.call_args.args[1] is norm.weight
