@@ -1,7 +1,8 @@
 /*
  * C ABI of the decoder operators around the attention (also in
  * libmt_attn.so): RMSNorm, residual-add + RMSNorm and the SwiGLU gate,
- * forward and backward, for MI355X (gfx950).  Plain pointers and sizes only.
+ * forward and backward, and the cross-entropy rows of the fused linear
+ * cross-entropy loss head, for MI355X (gfx950).  Plain pointers and sizes only.
  *
  * They replace these reference operators (src/mega_trading/kernels/triton_ops.py):
  *
@@ -17,6 +18,12 @@
  *                           reached from triton_swiglu_gate :57-61 and
  *                           SwiGLU.forward, src/mega_trading/model.py:252-253
  *   mt_swiglu_bwd        <- _TritonSwiGLUGate.backward :455-474 (kernel :799-819)
+ *   mt_cross_entropy_rows <- _fused_ce_row_kernel :822-887, the per-chunk loss and
+ *                           in-place logits-gradient step of
+ *                           _TritonFusedLinearCrossEntropy.forward :312-400,
+ *                           reached from triton_fused_linear_cross_entropy :64-92
+ *                           and TradingModel.forward_with_loss,
+ *                           src/mega_trading/model.py:113-123
  *
  * Conventions (as in mt_attention.h): device pointers on the current device,
  * asynchronous on `stream`, no allocation, no synchronisation; 0 = success,
@@ -76,6 +83,16 @@ int mt_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dt
 /* dgate = round(dout * up) * sig * (1 + gate (1 - sig)), dup = dout * round(silu(gate)). */
 int mt_swiglu_bwd(const void* gate, const void* up, const void* dout, void* dgate, void* dup, int64_t n, int dtype,
                   void* stream);
+
+/* Cross-entropy rows: for each of `rows` rows of `vocab` logits (row stride
+ * row_stride elements, dtype), loss_rows[r] = (logsumexp(row) - row[labels[r]]) / n_valid,
+ * with *n_valid (device int64) the number of labels != ignore_index; rows labelled
+ * ignore_index give 0.  With write_grad != 0 the logits are overwritten in place by
+ * (softmax(row) - onehot(label)) / n_valid (zero rows for ignored labels).  A label
+ * outside [0, vocab) gives a NaN loss.  vocab % 8 == 0; rows 16-byte aligned. */
+int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* labels, int64_t rows, int vocab,
+                          const int64_t* n_valid, int64_t ignore_index, float* loss_rows, int write_grad, int dtype,
+                          void* stream);
 
 #ifdef __cplusplus
 }

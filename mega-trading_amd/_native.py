@@ -35,6 +35,7 @@ EXPORTS = (
     "mt_add_rms_norm_bwd",
     "mt_swiglu_fwd",
     "mt_swiglu_bwd",
+    "mt_cross_entropy_rows",
 )
 
 _lock = threading.Lock()
@@ -55,6 +56,7 @@ _OPS_SIGNATURES = {
     "mt_add_rms_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
     "mt_swiglu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "mt_swiglu_bwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _P]),
+    "mt_cross_entropy_rows": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _I, _I, _P]),
 }
 
 

@@ -1,5 +1,6 @@
 // C ABI of the decoder operators (RMSNorm, residual-add + RMSNorm, SwiGLU
-// gate): argument checks, launch geometry and dispatch to ops_kernels.h.
+// gate, cross-entropy rows): argument checks, launch geometry and dispatch to
+// ops_kernels.h.
 // Declared in include/mt_ops.h.
 #include <hip/hip_runtime.h>
 
@@ -248,6 +249,32 @@ int mt_swiglu_bwd(const void* gate, const void* up, const void* dout, void* dgat
     hipLaunchKernelGGL((K::swiglu_bwd_kernel<K::kDtFP16>), grid, dim3(256), 0, st, gate, up, dout, dgate, dup, n);
   else
     hipLaunchKernelGGL((K::swiglu_bwd_kernel<K::kDtFP32>), grid, dim3(256), 0, st, gate, up, dout, dgate, dup, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* labels, int64_t rows, int vocab,
+                          const int64_t* n_valid, int64_t ignore_index, float* loss_rows, int write_grad, int dtype,
+                          void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, dtype))) return rc;
+  if (rows < 0 || rows > 0x7fffffffLL) return fail(MT_E_SHAPE, "rows must be in [0, 2^31) (got %lld)", (long long)rows);
+  if (vocab < 8 || vocab % 8) return fail(MT_E_SHAPE, "vocab %d unsupported (a positive multiple of 8)", vocab);
+  if (rows == 0) return ok();
+  if ((rc = check_ptr("logits", logits)) || (rc = check_stride("logits", row_stride, vocab))) return rc;
+  if (!labels || !n_valid || !loss_rows) return fail(MT_E_NULL, "labels, n_valid and loss_rows must be non-NULL");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)rows);
+  if (dtype == MT_DTYPE_BF16) {
+    if (write_grad) hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtBF16, true>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+    else hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtBF16, false>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+  } else if (dtype == MT_DTYPE_FP16) {
+    if (write_grad) hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP16, true>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+    else hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP16, false>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+  } else {
+    if (write_grad) hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP32, true>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+    else hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP32, false>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+  }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }

@@ -6,6 +6,7 @@
 //   RMSNorm          :11-15, :133-184, kernels :528-539 (forward), :633-666 (backward)
 //   add + RMSNorm    :18-42, :217-291, kernels :541-566, :569-608
 //   SwiGLU gate      :57-61, :431-474, kernels :774-782, :799-819
+//   cross-entropy rows of the fused linear cross-entropy :294-412, kernel :822-887
 //
 // All of them move each byte once: one wave owns one row (RMSNorm, rows of D
 // <= 4096 values held in registers as 8-value chunks), the SwiGLU gate streams
@@ -334,6 +335,88 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const
     const float sg = 1.f / (1.f + e);
     IO<DT>::store1(dgate, t, (IO<DT>::round(dy * u) * sg) * (1.f + g * (1.f - sg)));
     IO<DT>::store1(dup, t, dy * IO<DT>::round(g / (1.f + e)));
+  }
+}
+
+// ===========================================================================
+// Cross-entropy over rows of logits (the loss head of the fused linear
+// cross-entropy).  One workgroup per row of V logits:
+//   pass 1: running (max, sum of exp) over the row, combined across the 256
+//           threads;  lse = max + log(sum);  loss[row] = (lse - logit[label]) / n_valid
+//   pass 2 (GRAD): logits[row] <- (exp(logit - lse) - [j == label]) / n_valid,
+//           written over the logits in place (the second read hits the cache)
+// Rows whose label is ignore_index get loss 0 and (GRAD) a zero row.  n_valid is
+// read from device memory (no host synchronisation); n_valid = 0 gives zeros.  A
+// label outside [0, V) gives a NaN loss (the row is still read in bounds).
+// ===========================================================================
+struct MaxSum {
+  float m, s;
+};
+
+__device__ __forceinline__ MaxSum ms_combine(MaxSum a, MaxSum b) {
+  if (a.m == -INFINITY) return b;
+  if (b.m == -INFINITY) return a;
+  const float m = fmaxf(a.m, b.m);
+  return MaxSum{m, a.s * expf(a.m - m) + b.s * expf(b.m - m)};
+}
+
+template <int DT, bool GRAD>
+__global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, const int64_t* labels, int V,
+                                                      const int64_t* n_valid, int64_t ignore_index, float* loss) {
+  __shared__ MaxSum part[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t base = row * ld;
+  const int nvec = V >> 3;
+  const int64_t label = labels[row];
+  const int64_t nv = *n_valid;
+  const float inv_n = nv > 0 ? 1.f / float(nv) : 0.f;
+  if (label == ignore_index) {
+    if constexpr (GRAD) {
+      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int c = tid; c < nvec; c += 256) IO<DT>::store8(logits, base + 8 * c, z);
+    }
+    if (tid == 0) loss[row] = 0.f;
+    return;
+  }
+  MaxSum acc{-INFINITY, 0.f};
+  for (int c = tid; c < nvec; c += 256) {
+    float v[8];
+    IO<DT>::load8(logits, base + 8 * c, v);
+    float m = v[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) m = fmaxf(m, v[j]);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += expf(v[j] - m);
+    acc = ms_combine(acc, MaxSum{m, sum});
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    MaxSum other{__shfl_xor(acc.m, o, 64), __shfl_xor(acc.s, o, 64)};
+    acc = ms_combine(acc, other);
+  }
+  if ((tid & 63) == 0) part[tid >> 6] = acc;
+  __syncthreads();
+  const MaxSum tot = ms_combine(ms_combine(part[0], part[1]), ms_combine(part[2], part[3]));
+  const float lse = tot.m + logf(tot.s);
+  const bool ok = label >= 0 && label < V;
+  if (tid == 0) {
+    const float ly = IO<DT>::load1(logits, base + (ok ? label : 0));
+    loss[row] = ok ? (lse - ly) * inv_n : __builtin_nanf("");
+  }
+  if constexpr (GRAD) {
+    __syncthreads();  // the label's logit is read above before it is overwritten below
+    for (int c = tid; c < nvec; c += 256) {
+      float v[8];
+      IO<DT>::load8(logits, base + 8 * c, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = expf(v[j] - lse);
+        v[j] = (p - (8 * c + j == label ? 1.f : 0.f)) * inv_n;
+      }
+      IO<DT>::store8(logits, base + 8 * c, v);
+    }
   }
 }
 

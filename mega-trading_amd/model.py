@@ -21,8 +21,10 @@ takes the attention backend (``model.py:179-183, 252-253``), so "triton" /
 "hip" use the HIP gate (``ops.swiglu_gate``); the reference builds its RMSNorm
 modules without a backend (``model.py:166, 176``, torch ``F.rms_norm``), which
 "triton" keeps, while "hip" -- this package's own value -- also runs them on
-the HIP RMSNorm kernels (``ops.rms_norm``).  The loss head is torch
-``F.cross_entropy``.
+the HIP RMSNorm kernels (``ops.rms_norm``).  The loss head follows
+``model.py:113-123``: "triton" / "hip" without requested logits use the fused
+linear cross-entropy (``ops.fused_linear_cross_entropy``), everything else the
+torch ``F.linear`` + ``F.cross_entropy``.
 """
 
 from __future__ import annotations
@@ -35,6 +37,7 @@ from torch import nn
 
 from .attention import attention as _hip_attention
 from .attention import rope_attention as _hip_rope_attention
+from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
 from .ops import rms_norm as _hip_rms_norm
 from .ops import swiglu_gate as _hip_swiglu_gate
 
@@ -109,10 +112,15 @@ class TradingModel(nn.Module):
         return_logits: bool,
         ignore_index: int = -100,
     ) -> tuple[torch.Tensor, torch.Tensor | None]:
-        """Network plus next-token cross entropy (``model.py:84-131``, torch loss head)."""
+        """Network plus next-token cross entropy (``model.py:84-131``)."""
         if labels.shape != input_ids.shape:
             raise ValueError("labels must match input_ids shape")
-        logits = self.output(self._hidden(input_ids))
+        normalized = self._hidden(input_ids)
+        if self.operator_backend in HIP_BACKENDS and not return_logits:
+            loss = _hip_fused_linear_cross_entropy(normalized.reshape(-1, normalized.shape[-1]), self.output.weight,
+                                                   labels.reshape(-1), ignore_index=ignore_index)
+            return loss, None
+        logits = self.output(normalized)
         loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), labels.reshape(-1), ignore_index=ignore_index)
         return loss, (logits if return_logits else None)
 

@@ -20,7 +20,6 @@ import time
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from .model import TradingModel
 
@@ -72,10 +71,12 @@ class TrainStep:
         self.device = dev
 
     def __call__(self) -> torch.Tensor:
+        # the model's loss entry (model.py:84-131): for the "auto"/SDPA route it is
+        # exactly the trainer's logits + nn.CrossEntropyLoss (trainer.py:309,337-338);
+        # the "triton"/"hip" routes take the fused linear cross-entropy head there
         self.model.train()
         with torch.autocast(device_type=self.device.type, dtype=torch.bfloat16):
-            logits = self.model(self.input_ids)
-            loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), self.labels.reshape(-1))
+            loss, _ = self.model.forward_with_loss(self.input_ids, self.labels, return_logits=False)
         loss.backward()
         self.optimizer.step()
         self.optimizer.zero_grad(set_to_none=True)

@@ -26,6 +26,13 @@ Plain numpy restatements of the reference operators
 * ``swiglu_backward``       -- kernel ``:799-819``: ``t = round(dy * up)``,
                                ``dg = t * sig * (1 + g (1 - sig))``,
                                ``du = dy * round(silu(g))``.
+* ``cross_entropy_rows``    -- kernel ``:822-887``: per row ``lse = logsumexp(logits)``,
+                               ``loss = (lse - logits[label]) / n_valid`` and
+                               ``grad = (softmax - onehot(label)) / n_valid``; rows labelled
+                               ``ignore_index`` give 0 and a zero row.
+* ``fused_linear_cross_entropy`` -- ``:294-412``: the mean loss of ``hidden @ weight.T`` and
+                               its gradients ``grad_logits @ weight``, ``grad_logits.T @ hidden``,
+                               with the compute-dtype roundings of the inputs and logits.
 
 Arithmetic is float64 for the RMSNorm functions (compare with a tolerance) and
 float32 with explicit storage roundings for the SwiGLU gate (so 16-bit results
@@ -55,6 +62,8 @@ __all__ = [
     "add_rms_norm_backward",
     "swiglu_forward",
     "swiglu_backward",
+    "cross_entropy_rows",
+    "fused_linear_cross_entropy",
 ]
 
 
@@ -133,3 +142,33 @@ def swiglu_backward(g: np.ndarray, up: np.ndarray, dy: np.ndarray, dtype: str = 
     dg = round_to((t * sig) * (np.float32(1) + g * (np.float32(1) - sig)), dtype)
     du = round_to(dy * round_to(_silu32(g), dtype), dtype)
     return dg, du
+
+
+def cross_entropy_rows(logits: np.ndarray, labels: np.ndarray, ignore_index: int = -100):
+    """(loss per row, d loss / d logits) of ``triton_ops.py:822-887`` (float64)."""
+    x = np.asarray(logits, dtype=np.float64)
+    labels = np.asarray(labels, dtype=np.int64)
+    keep = labels != ignore_index
+    n_valid = int(keep.sum())
+    inv_n = 1.0 / n_valid if n_valid else 0.0
+    m = np.max(x, axis=-1, keepdims=True)
+    lse = (m + np.log(np.sum(np.exp(x - m), axis=-1, keepdims=True)))[:, 0]
+    rows = np.arange(x.shape[0])
+    safe = np.where(keep, labels, 0)
+    loss = np.where(keep, (lse - x[rows, safe]) * inv_n, 0.0)
+    grad = np.exp(x - lse[:, None])
+    grad[rows, safe] -= 1.0
+    grad *= inv_n
+    grad[~keep] = 0.0
+    return loss, grad
+
+
+def fused_linear_cross_entropy(hidden, weight, labels, ignore_index: int = -100, compute: str = "bfloat16"):
+    """(mean loss, d/d hidden, d/d weight) of ``triton_ops.py:294-412`` in float64 on
+    compute-dtype-rounded hidden and weight, with the logits rounded to that dtype
+    (the GEMM's output type) before the cross-entropy."""
+    h = round_to(np.asarray(hidden, dtype=np.float32), compute).astype(np.float64)
+    w = round_to(np.asarray(weight, dtype=np.float32), compute).astype(np.float64)
+    logits = round_to((h @ w.T).astype(np.float32), compute)
+    loss_rows, grad = cross_entropy_rows(logits, labels, ignore_index)
+    return float(np.sum(loss_rows)), grad @ w, grad.T @ h

@@ -79,6 +79,11 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     assert lib.mt_swiglu_fwd(p, p + 8, p, 100, BF16, None) == -3
     assert lib.mt_swiglu_bwd(p, p, None, p, p, 100, BF16, None) == -1
     assert lib.mt_swiglu_fwd(None, None, None, 0, BF16, None) == 0  # n = 0: nothing to do
+    assert lib.mt_cross_entropy_rows(p, 16, p, 4, 12, p, -100, p, 1, BF16, None) == -2  # vocab not a multiple of 8
+    assert lib.mt_cross_entropy_rows(p, 8, p, 4, 16, p, -100, p, 1, BF16, None) == -3  # row stride < vocab
+    assert lib.mt_cross_entropy_rows(p, 16, None, 4, 16, p, -100, p, 1, BF16, None) == -1
+    assert lib.mt_cross_entropy_rows(p, 16, p, -1, 16, p, -100, p, 1, BF16, None) == -2
+    assert lib.mt_cross_entropy_rows(None, 16, None, 0, 16, None, -100, None, 1, BF16, None) == 0
     assert lib.mt_last_error() == b""
 
 
@@ -90,6 +95,10 @@ def test_ops_reject_cpu_tensors(mta):
         mta.add_rms_norm(x, x, torch.ones(16), eps=1e-5)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         mta.swiglu_gate(x, x)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mta.ops.fused_linear_cross_entropy(x, torch.zeros(8, 16), torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(ValueError, match="one entry per hidden row"):
+        mta.ops.fused_linear_cross_entropy(x, torch.zeros(8, 16), torch.zeros(5, dtype=torch.int64))
 
 
 def test_kernel_timer_arming(mta):

@@ -183,3 +183,91 @@ def test_swiglu_errors(mta):
         mta.swiglu_gate(torch.zeros(4, device="cuda"), torch.zeros(5, device="cuda"))
     with pytest.raises(RuntimeError, match="dtype"):
         mta.swiglu_gate(torch.zeros(4, device="cuda", dtype=torch.float64), torch.zeros(4, device="cuda", dtype=torch.float64))
+
+
+# ---------------------------------------------------------------------------
+# fused linear cross-entropy (HIP cross-entropy rows between hipBLASLt GEMMs)
+# ---------------------------------------------------------------------------
+def _ce_case(rows, hdim, vocab, seed, ignore_every=0):
+    h = _gen((rows, hdim), seed, torch.float32)
+    w = _gen((vocab, hdim), seed + 1, torch.float32, 0.05)
+    g = torch.Generator().manual_seed(seed + 2)
+    labels = torch.randint(0, vocab, (rows,), generator=g)
+    if ignore_every:
+        labels[::ignore_every] = -100
+    return h, w, labels
+
+
+@pytest.mark.parametrize("compute", ["bfloat16", "float32"])
+def test_fused_linear_ce_vs_oracle(mta, compute):
+    h, w, labels = _ce_case(1000, 512, 16384, 60, ignore_every=9)
+    hg, wg = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=compute == "bfloat16"):
+        loss = mta.ops.fused_linear_cross_entropy(hg, wg, labels.cuda())
+    loss.backward()
+    assert loss.dtype == torch.float32 and hg.grad.dtype == torch.float32 and wg.grad.dtype == torch.float32
+    rl, rgh, rgw = oo.fused_linear_cross_entropy(h.numpy(), w.numpy(), labels.numpy(), -100, compute)
+    assert abs(loss.item() - rl) <= 1e-4 * abs(rl), (loss.item(), rl)
+    tol = 1e-2 if compute == "bfloat16" else 1e-4
+    assert _rel(hg.grad.cpu().numpy(), rgh) < tol
+    assert _rel(wg.grad.cpu().numpy(), rgw) < tol
+
+
+def test_fused_linear_ce_matches_eager_autocast_route_at_c5_rows(mta):
+    # the reference's eager loss head under bf16 autocast: F.linear + F.cross_entropy
+    # (model.py:124-129) on the C5 shape: 32 x 1024 rows, hidden 512, vocab 16384
+    h, w, labels = _ce_case(32 * 1024, 512, 16384, 61)
+    h, w, labels = h.cuda(), w.cuda(), labels.cuda()
+    ha, wa = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    hb, wb = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        la = mta.ops.fused_linear_cross_entropy(ha, wa, labels)
+        lb = F.cross_entropy(F.linear(hb, wb), labels)
+    la.backward()
+    lb.backward()
+    assert abs(la.item() - lb.item()) <= 1e-3 * abs(lb.item()), (la.item(), lb.item())
+    assert _rel(ha.grad.cpu().numpy(), hb.grad.cpu().numpy()) < 2e-2
+    assert _rel(wa.grad.cpu().numpy(), wb.grad.cpu().numpy()) < 2e-2
+
+
+def test_fused_linear_ce_edge_cases(mta):
+    h, w, labels = _ce_case(37, 64, 96, 62)
+    hg, wg = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+    # every row ignored: zero loss and zero gradients, as the reference
+    loss = mta.ops.fused_linear_cross_entropy(hg, wg, torch.full((37,), -100, device="cuda"))
+    loss.backward()
+    assert loss.item() == 0.0 and not hg.grad.any() and not wg.grad.any()
+    # int32 labels and a custom ignore_index; no-grad path returns the same loss
+    lab32 = labels.to(torch.int32).cuda()
+    lab32[3] = 7
+    with torch.no_grad():
+        l0 = mta.ops.fused_linear_cross_entropy(h.cuda(), w.cuda(), lab32, ignore_index=7)
+    l1 = mta.ops.fused_linear_cross_entropy(h.cuda().requires_grad_(True), w.cuda(), lab32, ignore_index=7)
+    assert torch.equal(l0, l1.detach())
+    rl, _, _ = oo.fused_linear_cross_entropy(h.numpy(), w.numpy(), lab32.cpu().numpy(), 7, "float32")
+    assert abs(l0.item() - rl) <= 1e-4 * abs(rl)
+    # a label outside [0, vocab) gives a NaN loss rather than a read out of bounds
+    bad = labels.clone().cuda()
+    bad[0] = 96
+    assert torch.isnan(mta.ops.fused_linear_cross_entropy(h.cuda(), w.cuda(), bad))
+    with pytest.raises(ValueError, match="multiple of 8"):
+        mta.ops.fused_linear_cross_entropy(h.cuda(), w[:90].cuda(), labels.cuda())
+
+
+def test_fused_linear_ce_chunked_equals_single_chunk(mta, monkeypatch):
+    # batches beyond the chunk budget are processed in row chunks: same loss and gradients
+    h, w, labels = _ce_case(3000, 128, 4096, 63, ignore_every=5)
+    outs = []
+    for budget in (2 << 30, 700 * 4096 * 2):  # one chunk; chunks of 700 rows (5 chunks, ragged last)
+        monkeypatch.setattr(mta.ops, "_CE_CHUNK_BYTES", budget)
+        hg, wg = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = mta.ops.fused_linear_cross_entropy(hg, wg, labels.cuda())
+        loss.backward()
+        outs.append((loss.detach(), hg.grad, wg.grad))
+    (l1, gh1, gw1), (l2, gh2, gw2) = outs
+    torch.testing.assert_close(l2, l1, rtol=1e-6, atol=1e-6)
+    # rows are independent, but the GEMM library may pick other tilings for other row counts
+    # (another accumulation order): equal to about a bf16 ulp
+    assert _rel(gh2.cpu().numpy(), gh1.cpu().numpy()) < 2e-3
+    assert _rel(gw2.cpu().numpy(), gw1.cpu().numpy()) < 5e-3  # summed per chunk in fp32 from bf16 products

@@ -170,3 +170,24 @@ def test_operator_routing_follows_the_reference(backend, gate_hip, norm_hip):
     assert rms.called == norm_hip
     if norm_hip:
         assert rms.call_args.kwargs["eps"] == 1e-5 and rms.call_args.args[1] is norm.weight
+
+
+
+@pytest.mark.parametrize("backend,fused", [("auto", False), ("triton", True), ("hip", True)])
+def test_loss_head_routing(backend, fused):
+    # model.py:113-123: the fused linear cross-entropy for the Triton route when logits are not requested
+    m = model_mod.TradingModel(vocab_size=32, block_size=8, hidden_dim=16, layers=1, attention_heads=4, kv_heads=2,
+                               dropout=0.0, rope_theta=10_000.0, attention_backend="auto")
+    m.operator_backend = backend  # keep the rest of the network on torch ops (CPU)
+    ids = torch.randint(0, 32, (2, 8))
+    with patch("mega-trading_amd.model._hip_fused_linear_cross_entropy", return_value=torch.tensor(1.5)) as ce:
+        loss, logits = m.forward_with_loss(ids, ids, return_logits=False)
+    assert ce.called == fused and logits is None
+    if fused:
+        hidden, weight, labels = ce.call_args.args
+        assert hidden.shape == (16, 16) and weight is m.output.weight and labels.shape == (16,)
+        assert ce.call_args.kwargs["ignore_index"] == -100 and loss.item() == 1.5
+    with patch("mega-trading_amd.model._hip_fused_linear_cross_entropy") as ce:
+        loss, logits = m.forward_with_loss(ids, ids, return_logits=True)  # logits requested: torch head
+    ce.assert_not_called()
+    assert logits.shape == (2, 8, 32)

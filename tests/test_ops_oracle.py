@@ -197,3 +197,74 @@ def test_swiglu_planted_mistakes_fail():
     sig = 1 / (1 + np.exp(-gb))
     bad_dg = oo.round_to(oo.round_to(dyb * ub, "bfloat16") * sig * (1 + gb), "bfloat16")
     assert not np.allclose(bad_dg, gg.grad.float().numpy(), rtol=1e-2, atol=1e-2)
+
+
+# ---------------------------------------------------------------------------
+# cross-entropy rows / fused linear cross-entropy
+# ---------------------------------------------------------------------------
+def _torch_ce(x, labels, ignore):
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    loss = F.cross_entropy(xt, torch.tensor(labels), ignore_index=ignore)
+    loss.backward()
+    return loss.item(), xt.grad.numpy()
+
+
+@pytest.mark.parametrize("ignore_frac", [0.0, 0.3])
+def test_cross_entropy_rows_match_torch(ignore_frac):
+    rng = np.random.default_rng(50)
+    x = rng.standard_normal((64, 40)) * 3
+    labels = rng.integers(0, 40, 64)
+    labels[rng.random(64) < ignore_frac] = -100
+    loss, grad = oo.cross_entropy_rows(x, labels, -100)
+    tl, tg = _torch_ce(x, labels, -100)
+    assert abs(loss.sum() - tl) < 1e-12
+    np.testing.assert_allclose(grad, tg, rtol=1e-12, atol=1e-14)
+
+
+def test_cross_entropy_closed_forms():
+    v = 24
+    loss, grad = oo.cross_entropy_rows(np.zeros((3, v)), np.array([0, 5, 23]))
+    np.testing.assert_allclose(loss.sum(), math.log(v))  # uniform logits: mean loss = log V
+    np.testing.assert_allclose(grad.sum(-1), 0.0, atol=1e-15)  # softmax minus onehot sums to 0
+    np.testing.assert_allclose(grad[1, 5], (1 / v - 1) / 3)
+    loss, grad = oo.cross_entropy_rows(np.ones((2, v)), np.array([-100, -100]))
+    assert loss.sum() == 0.0 and not grad.any()  # everything ignored: zeros
+    # shifting a row by a constant changes nothing
+    x = np.random.default_rng(51).standard_normal((4, v))
+    a = oo.cross_entropy_rows(x, np.array([1, 2, 3, 4]))
+    b = oo.cross_entropy_rows(x + 7.5, np.array([1, 2, 3, 4]))
+    np.testing.assert_allclose(a[0], b[0], rtol=1e-12)
+    np.testing.assert_allclose(a[1], b[1], rtol=1e-12, atol=1e-15)
+
+
+def test_cross_entropy_planted_mistakes_fail():
+    rng = np.random.default_rng(52)
+    x = rng.standard_normal((32, 16))
+    labels = rng.integers(0, 16, 32)
+    labels[:5] = -100
+    tl, tg = _torch_ce(x, labels, -100)
+    keep = labels != -100
+    lse = np.log(np.exp(x).sum(-1))
+    safe = np.where(keep, labels, 0)
+    by_rows = np.where(keep, lse - x[np.arange(32), safe], 0).sum() / 32  # normalised by all rows
+    assert abs(by_rows - tl) > 1e-3
+    shifted = np.where(keep, lse - x[np.arange(32), (safe + 1) % 16], 0).sum() / keep.sum()  # wrong column
+    assert abs(shifted - tl) > 1e-3
+    _, grad = oo.cross_entropy_rows(x, labels)
+    assert not np.allclose(np.exp(x - lse[:, None]) / keep.sum(), tg)  # no onehot term
+
+
+def test_fused_linear_ce_matches_torch_linear_plus_ce():
+    rng = np.random.default_rng(53)
+    h = rng.standard_normal((48, 32)).astype(np.float32)
+    w = (rng.standard_normal((64, 32)) * 0.2).astype(np.float32)
+    labels = rng.integers(0, 64, 48)
+    labels[::7] = -100
+    loss, gh, gw = oo.fused_linear_cross_entropy(h, w, labels, -100, "float32")
+    ht = torch.tensor(h, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    tl = F.cross_entropy(F.linear(ht, wt), torch.tensor(labels), ignore_index=-100)
+    tl.backward()
+    assert abs(loss - tl.item()) < 1e-6
+    np.testing.assert_allclose(gh, ht.grad.numpy(), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(gw, wt.grad.numpy(), rtol=1e-5, atol=1e-7)
