@@ -19,6 +19,8 @@
   train tokens/sec of the 8-layer decoder with the HIP
   attention in every layer against the same model on the reference's SDPA
   route (the "train tokens/sec" half of the metric).
+* ops: the decoder operators' HIP kernels (RMSNorm, SwiGLU gate, cross-entropy
+  rows) at their config 5 shapes, in GB/s against the 8 TB/s HBM peak.
 * mfma_ceiling: what this GPU sustains for back-to-back bf16 MFMA with random
   and with zero operands, and the shader clock it ran at (libmt_probe.so),
   measured right after the attention runs: under data-dependent MFMA load the
@@ -139,6 +141,75 @@ def mfma_ceiling(iters=20000, repeats=3):
         tf, mhz = res[len(res) // 2]
         out[name] = {"tflops": round(tf, 1), "clock_mhz": round(mhz), "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
     return out
+
+
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+
+
+def time_ops(pkg, iters=20):
+    """The decoder operators' HIP kernels at their BASELINE config 5 shapes
+    (rows = 32 x 1024 tokens): average time per launch (HIP events around
+    `iters` back-to-back launches on the current stream) and algorithmic HBM
+    bytes per launch over that time, against the 8 TB/s HBM peak."""
+    native = pkg._native
+    lib = native.load()
+    dev = torch.device("cuda:0")
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    rows, hid, inter, vocab = 32 * 1024, 512, 1408, 16384
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(rows, hid, device=dev, generator=g)
+    w = torch.ones(hid, device=dev)
+    y, dx, dy = torch.empty_like(x), torch.empty_like(x), torch.randn(rows, hid, device=dev, generator=g)
+    rstd = torch.empty(rows, device=dev)
+    dw = torch.empty_like(w)
+    ws_bytes = lib.mt_rms_norm_bwd_workspace_size(rows, hid)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    gate = torch.randn(rows, inter, device=dev, generator=g).to(torch.bfloat16)
+    up, dout = torch.randn_like(gate), torch.randn_like(gate)
+    out, dgate, dup = torch.empty_like(gate), torch.empty_like(gate), torch.empty_like(gate)
+    logits = torch.randn(rows, vocab, device=dev, generator=g).to(torch.bfloat16)
+    labels = torch.randint(0, vocab, (rows,), device=dev, generator=g)
+    n_valid = torch.tensor(rows, device=dev, dtype=torch.int64)
+    loss_rows = torch.empty(rows, device=dev)
+    f32, bf16 = native.DTYPE_FP32, native.DTYPE_BF16
+    mb = lambda n_elems, elem: n_elems * elem  # noqa: E731
+    cases = {
+        "rms_norm_fwd (fp32 32768x512)": (
+            lambda: lib.mt_rms_norm_fwd(x.data_ptr(), hid, w.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, hid,
+                                        1e-5, f32, f32, sp),
+            2 * mb(rows * hid, 4) + mb(rows, 4)),
+        "rms_norm_bwd (fp32 32768x512, + dW column sum)": (
+            lambda: lib.mt_rms_norm_bwd(x.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr(), dx.data_ptr(),
+                                        dw.data_ptr(), ws.data_ptr(), ws_bytes, rows, hid, f32, f32, sp),
+            3 * mb(rows * hid, 4) + mb(rows, 4)),
+        "swiglu_fwd (bf16 32768x1408)": (
+            lambda: lib.mt_swiglu_fwd(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(), bf16, sp),
+            3 * mb(gate.numel(), 2)),
+        "swiglu_bwd (bf16 32768x1408)": (
+            lambda: lib.mt_swiglu_bwd(gate.data_ptr(), up.data_ptr(), dout.data_ptr(), dgate.data_ptr(),
+                                      dup.data_ptr(), gate.numel(), bf16, sp),
+            5 * mb(gate.numel(), 2)),
+        "cross_entropy_rows (bf16 32768x16384, grad in place)": (
+            lambda: lib.mt_cross_entropy_rows(logits.data_ptr(), vocab, labels.data_ptr(), rows, vocab,
+                                              n_valid.data_ptr(), -100, loss_rows.data_ptr(), 1, bf16, sp),
+            2 * mb(rows * vocab, 2) + mb(rows, 12)),
+    }
+    res = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(3):
+            native.check(fn(), name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            native.check(fn(), name)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / iters * 1e3
+        gbps = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 1), "bytes": int(nbytes), "GBps": round(gbps, 1),
+                     "frac_hbm_peak": round(gbps / PEAK_HBM_GBPS, 3)}
+    return res
 
 
 def time_kernels(pkg, cfg, iters):
@@ -311,6 +382,16 @@ def train_tokens_per_second(pkg, steps, warmup):
     return out
 
 
+def _calibration_copy() -> None:
+    """One 256 MiB device-to-device copy: the reference dispatch that scales the
+    FETCH_SIZE / WRITE_SIZE counters of a profiling run to bytes."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -318,6 +399,9 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-train", action="store_true", help="skip the config 5 train-step tokens/sec leg")
+    ap.add_argument("--ops-only", action="store_true",
+                    help="profiling driver: run only the decoder operators' kernels at config 5 shapes, then a "
+                         "256 MiB device copy (counter calibration), and print their timings")
     ap.add_argument("--kernels-only", action="store_true",
                     help="profiling driver: run only the C3 kernels stage by stage, then a 256 MiB device copy "
                          "(the reference kernel for HBM-traffic counter calibration), and print their timings")
@@ -331,13 +415,15 @@ def main(argv=None) -> int:
     pkg = importlib.import_module("mega-trading_amd")
     pkg._native.load()
 
+    if args.ops_only:
+        ops_res = time_ops(pkg)
+        _calibration_copy()
+        print(json.dumps({"ops": ops_res, "copy_bytes_each_way": 256 << 20}), flush=True)
+        return 0
+
     if args.kernels_only:
         kern = time_kernels(pkg, C3, args.steps)
-        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
+        _calibration_copy()
         print(json.dumps({"kernels": kern, "copy_bytes_each_way": 256 << 20}), flush=True)
         return 0
 
@@ -353,6 +439,7 @@ def main(argv=None) -> int:
     ms_c2, _ = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)
     ms_c3_plain, _ = time_op_steps(pkg, C3, max(10, args.steps // 2), 3, rope=False)
     ceiling = mfma_ceiling()
+    ops_line = time_ops(pkg)
 
     line = {
         "metric": METRIC,
@@ -384,6 +471,7 @@ def main(argv=None) -> int:
         "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1), "stage_ms": round(x["stage_ms"], 4)}
                     for n, x in kern.items()},
         "mfma_ceiling": ceiling,
+        "ops": ops_line,
         "secondary": {
             "C2_fwd_bwd_tflops": round(fwd_bwd_flops(*C2[:1], C2[1], C2[2], C2[4]) / (ms_c2 * 1e-3) / 1e12, 2),
             "C2_ms_per_step": round(ms_c2, 4),

@@ -80,7 +80,7 @@ hipError_t bwd_launch(const void* s, const void* w, const float* rstd, const voi
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((K::column_sum_kernel<WT>), dim3((dim + 63) / 64), dim3(256), 0, st, partial,
+  hipLaunchKernelGGL((K::column_sum_kernel<WT>), dim3((dim + 63) / 64), dim3(64 * K::kColWaves), 0, st, partial,
                      rows > 0 ? nb : 0, dim, dw);
   return hipGetLastError();
 }
@@ -138,6 +138,28 @@ int swiglu_blocks(int64_t n) {
   const int64_t want = (nvec + 255) / 256;
   const int64_t cap = 8L * device_cus();
   return (int)(want < 1 ? 1 : want < cap ? want : cap);
+}
+
+// register-resident rows up to 2048 * 8 = 16384 logits, streamed beyond
+template <int DT, bool GRAD, int NCH>
+void ce_launch(dim3 grid, hipStream_t st, void* logits, int64_t ld, const int64_t* labels, int V, const int64_t* nv,
+               int64_t ignore, float* loss) {
+  hipLaunchKernelGGL((K::ce_rows_kernel<DT, GRAD, NCH>), grid, dim3(256), 0, st, logits, ld, labels, V, nv, ignore, loss);
+}
+
+template <int DT>
+void ce_dispatch(int nch, bool grad, dim3 grid, hipStream_t st, void* logits, int64_t ld, const int64_t* labels, int V,
+                 const int64_t* nv, int64_t ignore, float* loss) {
+  if (grad) {
+    if (nch <= 1) ce_launch<DT, true, 1>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+    else if (nch <= 2) ce_launch<DT, true, 2>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+    else if (nch <= 4) ce_launch<DT, true, 4>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+    else if (nch <= 8) ce_launch<DT, true, 8>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+    else ce_launch<DT, true, 0>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+  } else {
+    if (nch <= 8) ce_launch<DT, false, 8>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+    else ce_launch<DT, false, 0>(grid, st, logits, ld, labels, V, nv, ignore, loss);
+  }
 }
 
 int rms_bwd_common(const void* s, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* ws,
@@ -265,16 +287,10 @@ int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* label
   if (!labels || !n_valid || !loss_rows) return fail(MT_E_NULL, "labels, n_valid and loss_rows must be non-NULL");
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)rows);
-  if (dtype == MT_DTYPE_BF16) {
-    if (write_grad) hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtBF16, true>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
-    else hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtBF16, false>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
-  } else if (dtype == MT_DTYPE_FP16) {
-    if (write_grad) hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP16, true>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
-    else hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP16, false>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
-  } else {
-    if (write_grad) hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP32, true>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
-    else hipLaunchKernelGGL((K::ce_rows_kernel<K::kDtFP32, false>), grid, dim3(256), 0, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
-  }
+  const int nch = (vocab / 8 + 255) / 256;  // 8-value chunks per thread
+  if (dtype == MT_DTYPE_BF16) ce_dispatch<K::kDtBF16>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+  else if (dtype == MT_DTYPE_FP16) ce_dispatch<K::kDtFP16>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+  else ce_dispatch<K::kDtFP32>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }

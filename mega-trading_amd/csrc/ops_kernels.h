@@ -249,13 +249,15 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const void* s, const v
   }
 }
 
-// dw[d] = sum over nb partial rows, stored as WT.  A block owns 64 columns;
-// wave q sums rows q, q + 4, ... into 8 independent accumulators (8 loads in
-// flight per lane), then wave 0 adds the four quarter sums.  The order of every
-// addition is fixed, so the result is deterministic.
+// dw[d] = sum over nb partial rows, stored as WT.  A block of 16 waves owns 64
+// columns; wave q sums rows q, q + 16, ... into 8 independent accumulators (8
+// loads in flight per lane), then wave 0 adds the 16 wave sums.  The order of
+// every addition is fixed, so the result is deterministic.
+constexpr int kColWaves = 16;
+
 template <int WT>
-__global__ __launch_bounds__(256) void column_sum_kernel(const float* partial, int nb, int D, void* out) {
-  __shared__ float quarter[4][64];
+__global__ __launch_bounds__(64 * kColWaves) void column_sum_kernel(const float* partial, int nb, int D, void* out) {
+  __shared__ float part[kColWaves][64];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int d = blockIdx.x * 64 + lane;
@@ -263,16 +265,21 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float* partial, i
   if (d < D) {
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int b = wave;
-    for (; b + 28 < nb; b += 32) {
+    for (; b + 7 * kColWaves < nb; b += 8 * kColWaves) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) a[k] += partial[(int64_t)(b + 4 * k) * D + d];
+      for (int k = 0; k < 8; ++k) a[k] += partial[(int64_t)(b + kColWaves * k) * D + d];
     }
-    for (; b < nb; b += 4) a[0] += partial[(int64_t)b * D + d];
+    for (; b < nb; b += kColWaves) a[0] += partial[(int64_t)b * D + d];
     acc = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
   }
-  quarter[wave][lane] = acc;
+  part[wave][lane] = acc;
   __syncthreads();
-  if (wave == 0 && d < D) IO<WT>::store1(out, d, ((quarter[0][lane] + quarter[1][lane]) + quarter[2][lane]) + quarter[3][lane]);
+  if (wave == 0 && d < D) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < kColWaves; ++q) t += part[q][lane];
+    IO<WT>::store1(out, d, t);
+  }
 }
 
 // ===========================================================================
@@ -290,15 +297,29 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float* partial, i
 // ===========================================================================
 template <int DT>
 __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const void* gate, const void* up, void* out, int64_t n) {
+  // two 8-value chunks per thread per iteration, both loaded before any arithmetic
   const int64_t nvec = n >> 3;
   const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride) {
-    float g[8], u[8], o[8];
-    IO<DT>::load8(gate, 8 * i, g);
-    IO<DT>::load8(up, 8 * i, u);
+  for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < nvec; i0 += 2 * stride) {
+    float g[2][8], u[2][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[j] / (1.f + expf(-g[j]))) * u[j];
-    IO<DT>::store8(out, 8 * i, o);
+    for (int q = 0; q < 2; ++q) {
+      const int64_t i = i0 + q * stride;
+      if (i < nvec) {
+        IO<DT>::load8(gate, 8 * i, g[q]);
+        IO<DT>::load8(up, 8 * i, u[q]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t i = i0 + q * stride;
+      if (i < nvec) {
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[q][j] / (1.f + expf(-g[q][j]))) * u[q][j];
+        IO<DT>::store8(out, 8 * i, o);
+      }
+    }
   }
   const int64_t t = 8 * nvec + (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t < n && (int64_t)blockIdx.x * 256 + threadIdx.x < 8) {
@@ -312,21 +333,34 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const
                                                          void* dgate, void* dup, int64_t n) {
   const int64_t nvec = n >> 3;
   const int64_t stride = (int64_t)gridDim.x * 256;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride) {
-    float g[8], u[8], dy[8], dg[8], du[8];
-    IO<DT>::load8(gate, 8 * i, g);
-    IO<DT>::load8(up, 8 * i, u);
-    IO<DT>::load8(dout, 8 * i, dy);
+  for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < nvec; i0 += 2 * stride) {
+    float g[2][8], u[2][8], dy[2][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float e = expf(-g[j]);
-      const float sg = 1.f / (1.f + e);
-      const float t = IO<DT>::round(dy[j] * u[j]);
-      dg[j] = (t * sg) * (1.f + g[j] * (1.f - sg));
-      du[j] = dy[j] * IO<DT>::round(g[j] / (1.f + e));
+    for (int q = 0; q < 2; ++q) {
+      const int64_t i = i0 + q * stride;
+      if (i < nvec) {
+        IO<DT>::load8(gate, 8 * i, g[q]);
+        IO<DT>::load8(up, 8 * i, u[q]);
+        IO<DT>::load8(dout, 8 * i, dy[q]);
+      }
     }
-    IO<DT>::store8(dgate, 8 * i, dg);
-    IO<DT>::store8(dup, 8 * i, du);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t i = i0 + q * stride;
+      if (i < nvec) {
+        float dg[8], du[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float e = expf(-g[q][j]);
+          const float sg = 1.f / (1.f + e);
+          const float t = IO<DT>::round(dy[q][j] * u[q][j]);
+          dg[j] = (t * sg) * (1.f + g[q][j] * (1.f - sg));
+          du[j] = dy[q][j] * IO<DT>::round(g[q][j] / (1.f + e));
+        }
+        IO<DT>::store8(dgate, 8 * i, dg);
+        IO<DT>::store8(dup, 8 * i, du);
+      }
+    }
   }
   const int64_t t = 8 * nvec + (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t < n && (int64_t)blockIdx.x * 256 + threadIdx.x < 8) {
@@ -340,11 +374,15 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const
 
 // ===========================================================================
 // Cross-entropy over rows of logits (the loss head of the fused linear
-// cross-entropy).  One workgroup per row of V logits:
-//   pass 1: running (max, sum of exp) over the row, combined across the 256
+// cross-entropy).  One workgroup (256 threads) per row of V logits:
+//   pass 1: running (max, sum of exp) over the row, combined across the
 //           threads;  lse = max + log(sum);  loss[row] = (lse - logit[label]) / n_valid
 //   pass 2 (GRAD): logits[row] <- (exp(logit - lse) - [j == label]) / n_valid,
-//           written over the logits in place (the second read hits the cache)
+//           written over the logits in place
+// With NCH > 0 each thread keeps its NCH chunks of 8 logits in registers
+// between the passes (V <= 2048 * NCH: the row is read once); NCH == 0 streams
+// the row twice.  exp is the hardware exp2 (v_exp_f32 on x * log2 e), accurate
+// to a few fp32 ulps, far below the bf16 rounding of the logits.
 // Rows whose label is ignore_index get loss 0 and (GRAD) a zero row.  n_valid is
 // read from device memory (no host synchronisation); n_valid = 0 gives zeros.  A
 // label outside [0, V) gives a NaN loss (the row is still read in bounds).
@@ -357,10 +395,20 @@ __device__ __forceinline__ MaxSum ms_combine(MaxSum a, MaxSum b) {
   if (a.m == -INFINITY) return b;
   if (b.m == -INFINITY) return a;
   const float m = fmaxf(a.m, b.m);
-  return MaxSum{m, a.s * expf(a.m - m) + b.s * expf(b.m - m)};
+  return MaxSum{m, a.s * __expf(a.m - m) + b.s * __expf(b.m - m)};
 }
 
-template <int DT, bool GRAD>
+__device__ __forceinline__ MaxSum chunk_max_sum(const float* v) {
+  float m = v[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) m = fmaxf(m, v[j]);
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sum += __expf(v[j] - m);
+  return MaxSum{m, sum};
+}
+
+template <int DT, bool GRAD, int NCH>
 __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, const int64_t* labels, int V,
                                                       const int64_t* n_valid, int64_t ignore_index, float* loss) {
   __shared__ MaxSum part[4];
@@ -380,16 +428,21 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
     return;
   }
   MaxSum acc{-INFINITY, 0.f};
-  for (int c = tid; c < nvec; c += 256) {
-    float v[8];
-    IO<DT>::load8(logits, base + 8 * c, v);
-    float m = v[0];
+  float v[NCH > 0 ? NCH : 1][8];
+  if constexpr (NCH > 0) {
 #pragma unroll
-    for (int j = 1; j < 8; ++j) m = fmaxf(m, v[j]);
-    float sum = 0.f;
+    for (int k = 0; k < NCH; ++k) {
+      const int c = tid + 256 * k;
+      if (c < nvec) IO<DT>::load8(logits, base + 8 * c, v[k]);
+    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sum += expf(v[j] - m);
-    acc = ms_combine(acc, MaxSum{m, sum});
+    for (int k = 0; k < NCH; ++k)
+      if (tid + 256 * k < nvec) acc = ms_combine(acc, chunk_max_sum(v[k]));
+  } else {
+    for (int c = tid; c < nvec; c += 256) {
+      IO<DT>::load8(logits, base + 8 * c, v[0]);
+      acc = ms_combine(acc, chunk_max_sum(v[0]));
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -399,7 +452,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
   if ((tid & 63) == 0) part[tid >> 6] = acc;
   __syncthreads();
   const MaxSum tot = ms_combine(ms_combine(part[0], part[1]), ms_combine(part[2], part[3]));
-  const float lse = tot.m + logf(tot.s);
+  const float lse = tot.m + __logf(tot.s);
   const bool ok = label >= 0 && label < V;
   if (tid == 0) {
     const float ly = IO<DT>::load1(logits, base + (ok ? label : 0));
@@ -407,15 +460,25 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
   }
   if constexpr (GRAD) {
     __syncthreads();  // the label's logit is read above before it is overwritten below
-    for (int c = tid; c < nvec; c += 256) {
-      float v[8];
-      IO<DT>::load8(logits, base + 8 * c, v);
+    auto grad8 = [&](int c, float* x) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p = expf(v[j] - lse);
-        v[j] = (p - (8 * c + j == label ? 1.f : 0.f)) * inv_n;
+        const float p = __expf(x[j] - lse);
+        x[j] = (p - (8 * c + j == label ? 1.f : 0.f)) * inv_n;
       }
-      IO<DT>::store8(logits, base + 8 * c, v);
+      IO<DT>::store8(logits, base + 8 * c, x);
+    };
+    if constexpr (NCH > 0) {
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        const int c = tid + 256 * k;
+        if (c < nvec) grad8(c, v[k]);
+      }
+    } else {
+      for (int c = tid; c < nvec; c += 256) {
+        IO<DT>::load8(logits, base + 8 * c, v[0]);
+        grad8(c, v[0]);
+      }
     }
   }
 }

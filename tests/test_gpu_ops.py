@@ -271,3 +271,15 @@ def test_fused_linear_ce_chunked_equals_single_chunk(mta, monkeypatch):
     # (another accumulation order): equal to about a bf16 ulp
     assert _rel(gh2.cpu().numpy(), gh1.cpu().numpy()) < 2e-3
     assert _rel(gw2.cpu().numpy(), gw1.cpu().numpy()) < 5e-3  # summed per chunk in fp32 from bf16 products
+
+
+def test_cross_entropy_rows_streaming_vocab(mta):
+    # vocab above 16384 logits per row: the kernel streams the row twice instead of holding it in registers
+    h, w, labels = _ce_case(64, 64, 20000, 64, ignore_every=6)
+    hg, wg = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+    loss = mta.ops.fused_linear_cross_entropy(hg, wg, labels.cuda())
+    loss.backward()
+    rl, rgh, rgw = oo.fused_linear_cross_entropy(h.numpy(), w.numpy(), labels.numpy(), -100, "float32")
+    assert abs(loss.item() - rl) <= 1e-4 * abs(rl)
+    assert _rel(hg.grad.cpu().numpy(), rgh) < 1e-4
+    assert _rel(wg.grad.cpu().numpy(), rgw) < 1e-4
