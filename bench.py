@@ -19,6 +19,8 @@
   train tokens/sec of the 8-layer decoder with the HIP
   attention in every layer against the same model on the reference's SDPA
   route (the "train tokens/sec" half of the metric).
+* secondary.C5_generate: KV-cached generation on the HIP kernels against the
+  reference's per-token full recompute (model.py:134-147).
 * ops: the decoder operators' HIP kernels (RMSNorm, SwiGLU gate, cross-entropy
   rows) at their config 5 shapes, in GB/s against the 8 TB/s HBM peak.
 * mfma_ceiling: what this GPU sustains for back-to-back bf16 MFMA with random
@@ -392,6 +394,34 @@ def _calibration_copy() -> None:
     torch.cuda.synchronize()
 
 
+def generate_tokens_per_second(pkg, rollouts=32, prompt=512, new_tokens=64):
+    """Generation (the reference's TradingModel.generate, model.py:134-147, used by
+    eval and backtest): `rollouts` sequences from a `prompt`-token Zipf context,
+    `new_tokens` sampled tokens each (top-k 16), fp32 weights without autocast as
+    the reference's eval runs it.  hip = KV-cached decode on the HIP kernels;
+    reference = the full-context recompute loop on the SDPA route."""
+    wl = pkg.workload
+    ids, _ = wl.zipf_batch(rollouts, prompt, wl.C5_MODEL["vocab_size"], seed=3)
+    ids = ids.cuda()
+    out = {}
+    for name, backend in (("hip", "hip"), ("reference", "auto")):
+        model = wl.build_model(backend, seed=0, device="cuda").eval()
+        torch.manual_seed(0)
+        model.generate(ids, max_new_tokens=4)  # warm-up
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.generate(ids, max_new_tokens=new_tokens)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        out[name] = {"tokens_per_s": round(rollouts * new_tokens / dt, 1), "ms_per_token": round(dt / new_tokens * 1e3, 3)}
+        del model
+        torch.cuda.empty_cache()
+    out["speedup"] = round(out["hip"]["tokens_per_s"] / out["reference"]["tokens_per_s"], 3)
+    out["workload"] = (f"C5 decoder, {rollouts} rollouts x {new_tokens} new tokens after a {prompt}-token prompt, "
+                       "top-k 16 sampling, fp32 weights (no autocast)")
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -481,6 +511,7 @@ def main(argv=None) -> int:
     }
     if not args.no_train:
         line["secondary"]["C5_train"] = train_tokens_per_second(pkg, steps=20, warmup=5)
+        line["secondary"]["C5_generate"] = generate_tokens_per_second(pkg)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(C3)
     print(json.dumps(line), flush=True)

@@ -136,6 +136,24 @@ int mt_gqa_attn_bwd_dkv(const void* q, const void* k, const void* v, const void*
  */
 int mt_time_next_kernel(void* start_event, void* stop_event);
 
+/*
+ * Decode attention for KV-cached generation: one new query token per sequence
+ * (at position L-1) against cached keys/values 0..L-1.  It replaces the
+ * attention inside the per-token full recompute of TradingModel.generate,
+ * src/mega_trading/model.py:134-147 (model.py:139-140 runs the whole context
+ * through every layer for each new token): the result equals the last row of
+ * the causal forward over the L cached positions (triton_attention.py:28-78).
+ *   q [B,Hq,1,D] (rotated if RoPE is used), k_cache / v_cache [B,Hkv,>=L,D]
+ *   (rotated keys), o [B,Hq,1,D] written; strides: 16 int64 = q, k_cache,
+ *   v_cache, o in (b, h, t, d) order (the t stride of q and o is unused).
+ *   Hq / Hkv <= 8; L >= 1.  The fp32 workspace holds per-split partials
+ *   (mt_gqa_attn_decode_workspace_size).
+ */
+size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D);
+int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv,
+                       int L, int D, const int64_t* strides, float scale, int dtype, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,6 +8,8 @@ name carries a hyphen).  Public API:
 * ``rope_attention(query, key, value, cos, sin, *, repeats)`` -- the same with
   the interleaved RoPE of ``model.py:223`` fused into the kernels.
 * ``attention_forward(...)`` -- forward returning ``(output, logsumexp)``.
+* ``decode_attention(query, key_cache, value_cache, length, *, repeats)`` --
+  one new token against a KV cache (KV-cached ``generate``).
 * ``rms_norm``, ``add_rms_norm``, ``swiglu_gate`` -- the decoder's
   memory-bound operators (``triton_ops.py:11-61``) on HIP kernels (``ops``).
 * ``model`` -- the Llama-style order-flow decoder that calls them
@@ -16,8 +18,9 @@ name carries a hyphen).  Public API:
 """
 
 from . import model, ops, workload
-from .attention import SUPPORTED_HEAD_DIMS, attention, attention_forward, rope_attention
+from .attention import SUPPORTED_HEAD_DIMS, attention, attention_forward, decode_attention, rope_attention
 from .ops import add_rms_norm, rms_norm, swiglu_gate
 
-__all__ = ["attention", "rope_attention", "attention_forward", "SUPPORTED_HEAD_DIMS", "rms_norm", "add_rms_norm",
+__all__ = ["attention", "rope_attention", "attention_forward", "decode_attention", "SUPPORTED_HEAD_DIMS",
+           "rms_norm", "add_rms_norm",
            "swiglu_gate", "model", "ops", "workload"]

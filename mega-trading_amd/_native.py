@@ -36,6 +36,8 @@ EXPORTS = (
     "mt_swiglu_fwd",
     "mt_swiglu_bwd",
     "mt_cross_entropy_rows",
+    "mt_gqa_attn_decode_workspace_size",
+    "mt_gqa_attn_decode",
 )
 
 _lock = threading.Lock()
@@ -57,6 +59,8 @@ _OPS_SIGNATURES = {
     "mt_swiglu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "mt_swiglu_bwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _P]),
     "mt_cross_entropy_rows": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _I, _I, _P]),
+    "mt_gqa_attn_decode_workspace_size": (_S, [_I, _I, _I, _I]),
+    "mt_gqa_attn_decode": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _S, _P]),
 }
 
 

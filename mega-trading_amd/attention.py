@@ -25,7 +25,10 @@ import torch
 
 from . import _native
 
-__all__ = ["attention", "rope_attention", "attention_forward", "SUPPORTED_HEAD_DIMS"]
+__all__ = ["attention", "rope_attention", "attention_forward", "decode_attention", "SUPPORTED_HEAD_DIMS",
+           "MAX_DECODE_REPEATS"]
+
+MAX_DECODE_REPEATS = 8
 
 SUPPORTED_HEAD_DIMS = (32, 64, 128)
 _KERNEL_DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16}
@@ -88,6 +91,41 @@ def attention_forward(
             raise ValueError("cos and sin must be given together")
         c, s = _rope_tables(cos, sin, query)
     return _forward(query, key, value, c, s)
+
+
+def decode_attention(
+    query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, length: int, *, repeats: int
+) -> torch.Tensor:
+    """One new query token per sequence against a KV cache (inference only).
+
+    ``query`` [B, Hq, 1, D] is the new token's (rotated) query at position
+    ``length - 1``; ``key_cache`` / ``value_cache`` [B, Hkv, >= length, D] hold
+    the rotated keys and the values of positions 0 .. length-1 (the new token's
+    own included).  Returns [B, Hq, 1, D]: the last row of the causal GQA
+    attention over those positions (what ``TradingModel.generate``,
+    ``model.py:134-147``, obtains by recomputing the whole context).  16-bit
+    inputs; query head h reads KV head h // repeats; repeats <= 8.
+    """
+    if query.device.type != "cuda":
+        raise RuntimeError("hip attention backend requires ROCm GPU tensors")
+    if query.dtype not in _KERNEL_DTYPES:
+        raise RuntimeError("decode attention supports float16 and bfloat16 tensors")
+    if query.ndim != 4 or key_cache.ndim != 4 or value_cache.ndim != 4 or query.shape[2] != 1:
+        raise ValueError("query must be [batch, heads, 1, head_dim] and the caches [batch, heads, capacity, head_dim]")
+    if key_cache.shape != value_cache.shape:
+        raise ValueError("key and value caches must have the same shape")
+    if key_cache.shape[1] * repeats != query.shape[1] or repeats > MAX_DECODE_REPEATS:
+        raise ValueError(f"query heads must equal key/value heads multiplied by repeats (<= {MAX_DECODE_REPEATS})")
+    if key_cache.shape[0] != query.shape[0] or key_cache.shape[3] != query.shape[3]:
+        raise ValueError("query and caches must agree on batch and head_dim")
+    if not 1 <= length <= key_cache.shape[2]:
+        raise ValueError(f"length {length} outside [1, cache capacity {key_cache.shape[2]}]")
+    if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
+        raise RuntimeError("query and caches must share one dtype")
+    if query.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS} (got {query.shape[-1]})")
+    return torch.ops.mega_trading_amd.gqa_attn_decode(query, key_cache, value_cache, int(length),
+                                                      1.0 / math.sqrt(query.shape[-1]))
 
 
 # ---------------------------------------------------------------------------
@@ -259,6 +297,30 @@ def gqa_attn_bwd(
 @gqa_attn_bwd.register_fake
 def _gqa_attn_bwd_fake(q, k, v, o, lse, dout, cos, sin, scale):
     return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
+
+
+@torch.library.custom_op("mega_trading_amd::gqa_attn_decode", mutates_args=(), device_types="cuda")
+def gqa_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, length: int,
+                    scale: float) -> torch.Tensor:
+    lib = _native.load()
+    q, k_cache, v_cache = _kernel_ready(q), _kernel_ready(k_cache), _kernel_ready(v_cache)
+    b, hq, _, d = q.shape
+    hkv = k_cache.shape[1]
+    out = torch.empty((b, hq, 1, d), device=q.device, dtype=q.dtype)
+    strides = _strides(q, k_cache, v_cache, out)
+    with torch.cuda.device(q.device):
+        ws_bytes = lib.mt_gqa_attn_decode_workspace_size(b, hq, length, d)
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+        rc = lib.mt_gqa_attn_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), b, hq, hkv,
+                                    length, d, strides, scale, _KERNEL_DTYPES[q.dtype], ws.data_ptr(), ws_bytes,
+                                    torch.cuda.current_stream(q.device).cuda_stream)
+    _native.check(rc, "mt_gqa_attn_decode")
+    return out
+
+
+@gqa_attn_decode.register_fake
+def _gqa_attn_decode_fake(q, k_cache, v_cache, length, scale):
+    return q.new_empty(q.shape)
 
 
 def _fwd_setup_context(ctx, inputs, output):

@@ -1,0 +1,155 @@
+// gfx950 decode attention: one new query token per sequence against a KV cache,
+// for KV-cached generation (the reference's TradingModel.generate,
+// src/mega_trading/model.py:134-147, recomputes the whole context per token
+// instead; the maths is the causal GQA attention of triton_attention.py for the
+// last query row, whose keys are all cached positions).
+//
+// Split-K ("flash decoding"): the cached keys 0..L-1 are cut into 256-key
+// splits; workgroup (batch, KV head, split) scores its split for all R query
+// heads of the KV group (each K/V row is read once for the R heads), forms the
+// split's softmax numerator and running offset, and writes an fp32 partial
+// (o, m, l).  A second kernel merges the splits with the log-sum-exp rule.
+// The work is HBM-bound (the cache is read once), so it uses plain fp32 FMAs:
+// with one query row per head there is no matrix product to feed the MFMAs.
+#pragma once
+
+#include "mt_common.h"
+
+namespace mt {
+
+constexpr int kDecSplit = 256;  // keys per split (one per thread in the score pass)
+constexpr int kDecMaxR = 8;     // query heads per KV head supported
+
+struct DecodeParams {
+  const uint16_t* q;  // [B, Hq, 1, D] (rotated when RoPE is used)
+  const uint16_t* k;  // [B, Hkv, >= L, D] cache (rotated keys)
+  const uint16_t* v;  // [B, Hkv, >= L, D] cache
+  uint16_t* out;      // [B, Hq, 1, D]
+  float* part;        // [B, Hq, nsplit, D + 2] fp32: o (unnormalised), m (log2), l
+  int64_t sq[2], sk[3], sv[3], so[2];  // strides (b, h) for q / o, (b, h, t) for the caches
+  int B, Hq, Hkv, R, L, nsplit;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+template <class E, int D>
+__global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) {
+  __shared__ float qs[kDecMaxR][D];
+  __shared__ float ps[kDecMaxR][kDecSplit];
+  __shared__ float red[kDecMaxR][4];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int s = blockIdx.x % p.nsplit;
+  const int g = blockIdx.x / p.nsplit;
+  const int kvh = g % p.Hkv;
+  const int b = g / p.Hkv;
+  const int R = p.R;
+  const int k0 = s * kDecSplit;
+  const int n = min(kDecSplit, p.L - k0);
+
+  for (int i = tid; i < R * D; i += 256) {
+    const int h = i / D, d = i % D;
+    qs[h][d] = E::to_f(p.q[b * p.sq[0] + (int64_t)(kvh * R + h) * p.sq[1] + d]);
+  }
+  __syncthreads();
+
+  // scores of key k0 + tid for every head (log2 units)
+  float sc[kDecMaxR];
+#pragma unroll
+  for (int h = 0; h < kDecMaxR; ++h) sc[h] = 0.f;
+  if (tid < n) {
+    const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + tid) * p.sk[2];
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(krow + 8 * c);
+      float kv[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kv[2 * e] = lo_f<E>(w[e]);
+        kv[2 * e + 1] = hi_f<E>(w[e]);
+      }
+#pragma unroll
+      for (int h = 0; h < kDecMaxR; ++h)
+        if (h < R)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sc[h] = __builtin_fmaf(qs[h][8 * c + e], kv[e], sc[h]);
+    }
+  }
+  // per-head max over the split
+#pragma unroll
+  for (int h = 0; h < kDecMaxR; ++h) {
+    if (h >= R) break;
+    float v = tid < n ? sc[h] * p.scale_log2 : -INFINITY;
+    sc[h] = v;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if (lane == 0) red[h][wave] = v;
+  }
+  __syncthreads();
+  float m[kDecMaxR];
+#pragma unroll
+  for (int h = 0; h < kDecMaxR; ++h)
+    m[h] = h < R ? fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3])) : 0.f;
+  __syncthreads();  // red is reused for the sums
+  // probabilities (0 past the split's last key) and their per-head sums
+#pragma unroll
+  for (int h = 0; h < kDecMaxR; ++h) {
+    if (h >= R) break;
+    const float e = tid < n ? exp2_fast(sc[h] - m[h]) : 0.f;
+    ps[h][tid] = e;
+    float v = e;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (lane == 0) red[h][wave] = v;
+  }
+  __syncthreads();
+
+  // o[h][d] = sum_j p[h][j] V[k0 + j][d]: a wave reads V rows coalesced along d
+  const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2];
+  for (int i = tid; i < R * D; i += 256) {
+    const int h = i / D, d = i % D;
+    float acc = 0.f;
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      const float v0 = E::to_f(vbase[(int64_t)(j + 0) * p.sv[2] + d]);
+      const float v1 = E::to_f(vbase[(int64_t)(j + 1) * p.sv[2] + d]);
+      const float v2 = E::to_f(vbase[(int64_t)(j + 2) * p.sv[2] + d]);
+      const float v3 = E::to_f(vbase[(int64_t)(j + 3) * p.sv[2] + d]);
+      acc = __builtin_fmaf(ps[h][j], v0, acc);
+      acc = __builtin_fmaf(ps[h][j + 1], v1, acc);
+      acc = __builtin_fmaf(ps[h][j + 2], v2, acc);
+      acc = __builtin_fmaf(ps[h][j + 3], v3, acc);
+    }
+    for (; j < n; ++j) acc = __builtin_fmaf(ps[h][j], E::to_f(vbase[(int64_t)j * p.sv[2] + d]), acc);
+    float* dst = p.part + (((int64_t)b * p.Hq + kvh * R + h) * p.nsplit + s) * (D + 2);
+    dst[d] = acc;
+    if (d == 0) {
+      dst[D] = m[h];
+      dst[D + 1] = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+    }
+  }
+}
+
+// Merge the splits of each (batch, query head): M = max m_s,
+// O = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.  One thread per d value.
+template <class E, int D>
+__global__ __launch_bounds__(256) void attn_decode_combine_kernel(DecodeParams p) {
+  constexpr int PER = 256 / D;  // (batch, head) pairs per workgroup
+  const int pair = blockIdx.x * PER + threadIdx.x / D;
+  const int d = threadIdx.x % D;
+  if (pair >= p.B * p.Hq) return;
+  const int b = pair / p.Hq, h = pair % p.Hq;
+  const float* src = p.part + (int64_t)pair * p.nsplit * (D + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, src[s * (D + 2) + D]);
+  float o = 0.f, l = 0.f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const float w = exp2_fast(src[s * (D + 2) + D] - M);
+    o = __builtin_fmaf(w, src[s * (D + 2) + d], o);
+    l = __builtin_fmaf(w, src[s * (D + 2) + D + 1], l);
+  }
+  const float r = o / l;
+  p.out[b * p.so[0] + (int64_t)h * p.so[1] + d] = uint16_t(pack2<E>(r, 0.f) & 0xffffu);
+}
+
+}  // namespace mt

@@ -13,6 +13,7 @@
 
 #include "../../include/mt_attention.h"
 #include "attn_kernels.h"
+#include "decode_kernels.h"
 #include "mt_abi.h"
 
 namespace mt_abi {
@@ -262,7 +263,7 @@ int bwd_impl(int stage, const void* q, const void* k, const void* v, const void*
 
 extern "C" {
 
-int mt_version(void) { return (0 << 16) | 3; }
+int mt_version(void) { return (0 << 16) | 4; }
 
 const char* mt_last_error(void) { return mt_abi::last_error(); }
 
@@ -329,5 +330,55 @@ int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float*
 int mt_gqa_attn_bwd(MT_BWD_ARGS) { return bwd_impl(3, MT_BWD_PASS); }
 int mt_gqa_attn_bwd_dq(MT_BWD_ARGS) { return bwd_impl(1, MT_BWD_PASS); }
 int mt_gqa_attn_bwd_dkv(MT_BWD_ARGS) { return bwd_impl(2, MT_BWD_PASS); }
+
+size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D) {
+  if (B < 1 || Hq < 1 || L < 1 || D < 1) return 0;
+  const size_t nsplit = (size_t)((L + mt::kDecSplit - 1) / mt::kDecSplit);
+  return ((size_t)B * Hq * nsplit * (D + 2) * sizeof(float) + 255) / 256 * 256;
+}
+
+int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv, int L,
+                       int D, const int64_t* strides, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  int rc = check_common(B, Hq, Hkv, L, D, dtype, nullptr, nullptr);
+  if (rc) return rc;
+  if (Hq / Hkv > mt::kDecMaxR)
+    return fail(MT_E_SHAPE, "decode supports up to %d query heads per KV head (got %d)", mt::kDecMaxR, Hq / Hkv);
+  if (!strides) return fail(MT_E_NULL, "strides is NULL");
+  if ((rc = check_tensor("q", q, strides)) || (rc = check_tensor("k_cache", k_cache, strides + 4)) ||
+      (rc = check_tensor("v_cache", v_cache, strides + 8)) || (rc = check_tensor("o", o, strides + 12)))
+    return rc;
+  if (!workspace) return fail(MT_E_NULL, "workspace is NULL");
+  if (workspace_bytes < mt_gqa_attn_decode_workspace_size(B, Hq, L, D))
+    return fail(MT_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                mt_gqa_attn_decode_workspace_size(B, Hq, L, D));
+  mt::DecodeParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k_cache);
+  p.v = static_cast<const uint16_t*>(v_cache);
+  p.out = static_cast<uint16_t*>(o);
+  p.part = static_cast<float*>(workspace);
+  p.sq[0] = strides[0]; p.sq[1] = strides[1];
+  p.sk[0] = strides[4]; p.sk[1] = strides[5]; p.sk[2] = strides[6];
+  p.sv[0] = strides[8]; p.sv[1] = strides[9]; p.sv[2] = strides[10];
+  p.so[0] = strides[12]; p.so[1] = strides[13];
+  p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.R = Hq / Hkv; p.L = L;
+  p.nsplit = (L + mt::kDecSplit - 1) / mt::kDecSplit;
+  p.scale_log2 = scale * mt::kLog2e;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid_s((unsigned)(B * Hkv * p.nsplit));
+  const dim3 grid_c((unsigned)(((int64_t)B * Hq * D + 255) / 256));
+#define MT_DECODE_LAUNCH(E, DD)                                                                 \
+  hipLaunchKernelGGL((mt::attn_decode_split_kernel<E, DD>), grid_s, dim3(256), 0, st, p);     \
+  hipLaunchKernelGGL((mt::attn_decode_combine_kernel<E, DD>), grid_c, dim3(256), 0, st, p)
+  if (dtype == MT_DTYPE_BF16) {
+    if (D == 32) { MT_DECODE_LAUNCH(mt::BF16, 32); } else if (D == 64) { MT_DECODE_LAUNCH(mt::BF16, 64); } else { MT_DECODE_LAUNCH(mt::BF16, 128); }
+  } else {
+    if (D == 32) { MT_DECODE_LAUNCH(mt::FP16, 32); } else if (D == 64) { MT_DECODE_LAUNCH(mt::FP16, 64); } else { MT_DECODE_LAUNCH(mt::FP16, 128); }
+  }
+#undef MT_DECODE_LAUNCH
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "decode launch failed: %s", hipGetErrorString(e));
+}
 
 }  // extern "C"

@@ -35,7 +35,9 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from .attention import _rope_tables
 from .attention import attention as _hip_attention
+from .attention import decode_attention as _hip_decode_attention
 from .attention import rope_attention as _hip_rope_attention
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
 from .ops import rms_norm as _hip_rms_norm
@@ -123,6 +125,67 @@ class TradingModel(nn.Module):
         logits = self.output(normalized)
         loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), labels.reshape(-1), ignore_index=ignore_index)
         return loss, (logits if return_logits else None)
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, top_k: int = 16) -> torch.Tensor:
+        """Sample ``max_new_tokens`` tokens (top-k, multinomial) after ``input_ids``
+        (``model.py:134-147``).
+
+        The reference re-runs the whole context (the last ``block_size`` tokens)
+        through the model for every new token.  The HIP routes ("triton" / "hip")
+        instead keep a KV cache: one prefill over the prompt records every
+        layer's rotated keys and values, then each new token runs through the
+        model alone and attends to the cache (``decode_attention``).  The logits
+        are those of the full recompute (same causal attention, computed once).
+        When the sequence outgrows ``block_size`` the reference's window slides
+        and renumbers the RoPE positions, so from then on these routes recompute
+        the window as the reference does.  Other backends run the reference loop.
+        """
+        self.eval()
+        if self.operator_backend not in HIP_BACKENDS:
+            return self._generate_recompute(input_ids, max_new_tokens, top_k)
+        tokens = input_ids
+        cache = None
+        for _ in range(max_new_tokens):
+            t = tokens.shape[1]
+            if t > self.block_size:
+                cache = None
+                logits = self(tokens[:, -self.block_size:])[:, -1, :]
+            elif cache is None:
+                logits, cache = self._prefill(tokens)
+            else:
+                logits = self._decode(tokens[:, -1:], cache, t - 1)
+            tokens = torch.cat([tokens, _sample_next(logits, top_k)], dim=1)
+        return tokens
+
+    @torch.no_grad()
+    def _generate_recompute(self, input_ids: torch.Tensor, max_new_tokens: int, top_k: int) -> torch.Tensor:
+        """The reference's loop (``model.py:136-147``): the whole window per token."""
+        self.eval()
+        tokens = input_ids
+        for _ in range(max_new_tokens):
+            logits = self(tokens[:, -self.block_size:])[:, -1, :]
+            tokens = torch.cat([tokens, _sample_next(logits, top_k)], dim=1)
+        return tokens
+
+    def _prefill(self, tokens: torch.Tensor):
+        """Forward over the prompt that also returns per-layer KV caches of capacity block_size."""
+        hidden = self.token_embedding(tokens)
+        cache = []
+        for block in self.blocks:
+            attended, k_cache, v_cache = block.attention.prefill(block.attention_norm(hidden), self.block_size)
+            cache.append((k_cache, v_cache))
+            hidden = hidden + attended
+            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
+        return self.output(self.norm(hidden))[:, -1, :], cache
+
+    def _decode(self, token: torch.Tensor, cache, pos: int) -> torch.Tensor:
+        """Logits after the token at position ``pos`` (its K/V are appended to the caches)."""
+        hidden = self.token_embedding(token)
+        for block, (k_cache, v_cache) in zip(self.blocks, cache):
+            hidden = hidden + block.attention.decode(block.attention_norm(hidden), k_cache, v_cache, pos)
+            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
+        return self.output(self.norm(hidden))[:, -1, :]
 
     def _hidden(self, input_ids: torch.Tensor) -> torch.Tensor:
         if input_ids.ndim != 2:
@@ -225,6 +288,46 @@ class LlamaAttention(nn.Module):
         attended = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, hidden_dim)
         return self.o_proj(attended)
 
+    def _heads(self, hidden: torch.Tensor):
+        b, t, _ = hidden.shape
+        query = self.q_proj(hidden).view(b, t, self.attention_heads, self.head_dim).transpose(1, 2)
+        key = self.k_proj(hidden).view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
+        value = self.v_proj(hidden).view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
+        return query, key, value
+
+    def prefill(self, hidden: torch.Tensor, capacity: int):
+        """Attention over the prompt (fused-RoPE HIP kernels) plus KV caches
+        [B, Hkv, capacity, D] holding its rotated keys and values (16-bit)."""
+        b, t, hidden_dim = hidden.shape
+        query, key, value = self._heads(hidden)
+        kdt = query.dtype if query.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+        q16, k16, v16 = query.to(kdt), key.to(kdt), value.to(kdt)
+        cos, sin = _rope_tables(self.rope.cos, self.rope.sin, q16)
+        out, _lse, _q_rot, k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(
+            q16, k16, v16, cos, sin, 1.0 / math.sqrt(self.head_dim))
+        k_cache = torch.empty((b, self.kv_heads, capacity, self.head_dim), device=hidden.device, dtype=kdt)
+        v_cache = torch.empty_like(k_cache)
+        k_cache[:, :, :t] = k_rot
+        v_cache[:, :, :t] = v16
+        attended = out.to(hidden.dtype).transpose(1, 2).contiguous().view(b, t, hidden_dim)
+        return self.o_proj(attended), k_cache, v_cache
+
+    def decode(self, hidden: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int) -> torch.Tensor:
+        """One token at position ``pos``: rotate its q/k (fp32 from the 16-bit
+        values, as the fused kernels do), append k/v to the caches, attend."""
+        b, _, hidden_dim = hidden.shape
+        query, key, value = self._heads(hidden)
+        kdt = k_cache.dtype
+        cos = self.rope.cos[0, 0, pos:pos + 1]
+        sin = self.rope.sin[0, 0, pos:pos + 1]
+        q_rot = rotate(query.to(kdt).float(), cos, sin).to(kdt)
+        k_rot = rotate(key.to(kdt).float(), cos, sin).to(kdt)
+        k_cache[:, :, pos] = k_rot[:, :, 0]
+        v_cache[:, :, pos] = value[:, :, 0].to(kdt)
+        out = _hip_decode_attention(q_rot, k_cache, v_cache, pos + 1, repeats=self.repeats)
+        attended = out.to(hidden.dtype).transpose(1, 2).reshape(b, 1, hidden_dim)
+        return self.o_proj(attended)
+
 
 class SwiGLU(nn.Module):
     """w2(silu(w1 x) * w3 x) (``model.py:240-256``); the gate on HIP for "triton" / "hip"."""
@@ -287,6 +390,15 @@ class RotaryEmbedding(nn.Module):
         cos = self.cos[:, :, :sequence_length].to(dtype=query.dtype)
         sin = self.sin[:, :, :sequence_length].to(dtype=query.dtype)
         return rotate(query, cos, sin), rotate(key, cos, sin)
+
+
+def _sample_next(logits: torch.Tensor, top_k: int) -> torch.Tensor:
+    """Top-k filtered multinomial sample of one token per row (``model.py:141-145``)."""
+    if top_k > 0:
+        values, _ = torch.topk(logits, min(top_k, logits.shape[-1]))
+        logits = logits.masked_fill(logits < values[:, [-1]], float("-inf"))
+    probs = torch.softmax(logits, dim=-1)
+    return torch.multinomial(probs, num_samples=1)
 
 
 def rotate(value: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:

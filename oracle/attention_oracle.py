@@ -26,6 +26,10 @@ attention algorithm.  Every function cites the reference line it follows
                           ``rowsum(dP * P)``).
 * ``rope_attention_forward/backward`` -- ``model.py:223-226`` (RoPE on q and k,
                           then attention), with the chain rule through the rotation.
+* ``decode_attention``   -- the last query row of ``attention_forward`` over the
+                          ``length`` cached positions: what ``TradingModel.generate``
+                          (``model.py:134-147``) computes for each new token by
+                          re-running the whole context.
 
 How each part is pinned (tests/test_oracle.py):
 
@@ -247,3 +251,24 @@ def rope_attention_backward(
     kr = apply_rope(k.astype(dtype), c, s)
     dq, dk, dv = attention_backward(qr, kr, v, do, repeats, scale, dtype)
     return rope_inverse(dq, c, s), rope_inverse(dk, c, s), dv
+
+
+def decode_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, length: int, repeats: int,
+                     scale: float | None = None, dtype=np.float64) -> np.ndarray:
+    """One query per (batch, head) at position ``length - 1`` against keys/values
+    0 .. length-1: ``softmax(scale q k^T) v`` (no mask is needed: every cached
+    position precedes the query).  q [B, Hq, D]; k, v [B, Hkv, >= length, D];
+    returns [B, Hq, D]."""
+    b, hq, d = q.shape
+    if k.shape[1] * repeats != hq:
+        raise ValueError("query heads must equal key/value heads multiplied by repeats")
+    if scale is None:
+        scale = 1.0 / np.sqrt(d)
+    out = np.empty((b, hq, d), dtype=dtype)
+    for bi in range(b):
+        for h in range(hq):
+            kk = k[bi, h // repeats, :length].astype(dtype)
+            s = (kk @ q[bi, h].astype(dtype)) * dtype(scale)
+            p = np.exp(s - s.max())
+            out[bi, h] = (p @ v[bi, h // repeats, :length].astype(dtype)) / p.sum()
+    return out

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol(mta):
     assert declared == sorted(mta._native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/mt_attention.h but not exported"
-    assert lib.mt_version() == (0 << 16) | 3
+    assert lib.mt_version() == (0 << 16) | 4
 
 
 def test_probe_library_exports_the_mfma_probe():

@@ -191,3 +191,19 @@ def test_loss_head_routing(backend, fused):
         loss, logits = m.forward_with_loss(ids, ids, return_logits=True)  # logits requested: torch head
     ce.assert_not_called()
     assert logits.shape == (2, 8, 32)
+
+
+def test_generate_reference_loop_on_cpu():
+    # the "auto" route keeps the reference's recompute loop (model.py:134-147), window included
+    m = model_mod.TradingModel(vocab_size=32, block_size=8, hidden_dim=16, layers=1, attention_heads=4, kv_heads=2,
+                               dropout=0.1, rope_theta=10_000.0)
+    ids = torch.randint(0, 32, (3, 5))
+    torch.manual_seed(0)
+    a = m.generate(ids, max_new_tokens=6, top_k=4)  # crosses block_size: the window slides
+    torch.manual_seed(0)
+    b = m._generate_recompute(ids, 6, 4)
+    assert a.shape == (3, 11) and torch.equal(a[:, :5], ids) and torch.equal(a, b)
+    assert int(a.max()) < 32 and not m.training
+    # top_k = 1 is greedy: the first new token is the argmax of the prompt's last logits
+    g = m.generate(ids, max_new_tokens=1, top_k=1)
+    assert torch.equal(g[:, -1], m(ids)[:, -1, :].argmax(-1))

@@ -322,3 +322,20 @@ def test_mutation_checks_are_sensitive():
     half = np.concatenate([x[..., :4] * cos - x[..., 4:] * sin, x[..., :4] * sin + x[..., 4:] * cos], -1)
     ang = 3 * 10_000.0 ** (-2 / 8)
     assert not np.isclose(half[0, 0, 3, 2], x[0, 0, 3, 2] * np.cos(ang) - x[0, 0, 3, 3] * np.sin(ang))
+
+
+
+def test_decode_oracle_is_the_last_row_of_the_causal_forward():
+    # pinned by the (already pinned) causal forward: the new token's output is the
+    # last row of attention over all cached positions, for every prefix length
+    rng = np.random.default_rng(70)
+    b, hq, hkv, t, d = 2, 8, 2, 19, 32
+    q = rng.standard_normal((b, hq, t, d))
+    k = rng.standard_normal((b, hkv, t, d))
+    v = rng.standard_normal((b, hkv, t, d))
+    for length in (1, 2, 7, 19):
+        full, _ = orc.attention_forward(q[:, :, :length], k[:, :, :length], v[:, :, :length], 4)
+        dec = orc.decode_attention(q[:, :, length - 1], k, v, length, 4)
+        np.testing.assert_allclose(dec, full[:, :, -1], rtol=1e-12, atol=1e-12)
+    # length 1: the output is v_0 exactly (one key)
+    np.testing.assert_allclose(orc.decode_attention(q[:, :, 0], k, v, 1, 4)[:, 0], v[:, 0, 0], rtol=1e-15)
