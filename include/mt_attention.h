@@ -153,6 +153,30 @@ size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D);
 int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv,
                        int L, int D, const int64_t* strides, float scale, int dtype, void* workspace,
                        size_t workspace_bytes, void* stream);
+/* As mt_gqa_attn_decode with the length read from device memory (*length_dev,
+ * clamped to [1, capacity]) when the kernels run, so one recorded launch
+ * (e.g. in a HIP graph) serves every decode step; the grid and the workspace
+ * (mt_gqa_attn_decode_workspace_size(B, Hq, capacity, D)) cover the capacity. */
+int mt_gqa_attn_decode_dev(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv,
+                           int capacity, const int* length_dev, int D, const int64_t* strides, float scale, int dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The decode step's RoPE and cache append (no reference counterpart as one
+ * call: it is the per-token share of model.py:223's rotation plus the cache
+ * write that KV-cached generation adds).  q [B,Hq,D], k/v [B,Hkv,D] (views of
+ * the new token's projections, in_strides: 6 int64 = (b, h) of q, k, v; d
+ * stride 1; in_dtype bf16, fp16 or 2 = fp32) are rounded to the cache dtype,
+ * rotated by position `pos` (fp32 tables [>= pos+1, D/2]) and written: q_rot
+ * [B,Hq,1,D] contiguous, k_cache[:, :, pos] and v_cache[:, :, pos]
+ * (cache_strides: 6 int64 = (b, h, t) of k_cache, v_cache).  With pos_dev set
+ * the position is read from device memory when the kernel runs, clamped to
+ * [0, pos] (pass the last valid position as pos).
+ */
+int mt_decode_rope_append(const void* q, const void* k, const void* v, const int64_t* in_strides,
+                          const float* rope_cos, const float* rope_sin, int pos, const int* pos_dev, void* q_rot,
+                          void* k_cache, void* v_cache, const int64_t* cache_strides, int B, int Hq, int Hkv, int D,
+                          int in_dtype, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,8 @@ EXPORTS = (
     "mt_cross_entropy_rows",
     "mt_gqa_attn_decode_workspace_size",
     "mt_gqa_attn_decode",
+    "mt_gqa_attn_decode_dev",
+    "mt_decode_rope_append",
 )
 
 _lock = threading.Lock()
@@ -61,6 +63,8 @@ _OPS_SIGNATURES = {
     "mt_cross_entropy_rows": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _I, _I, _P]),
     "mt_gqa_attn_decode_workspace_size": (_S, [_I, _I, _I, _I]),
     "mt_gqa_attn_decode": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _S, _P]),
+    "mt_gqa_attn_decode_dev": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _F, _I, _P, _S, _P]),
+    "mt_decode_rope_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
 }
 
 

@@ -94,7 +94,7 @@ def attention_forward(
 
 
 def decode_attention(
-    query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, length: int, *, repeats: int
+    query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor, length, *, repeats: int
 ) -> torch.Tensor:
     """One new query token per sequence against a KV cache (inference only).
 
@@ -105,6 +105,11 @@ def decode_attention(
     attention over those positions (what ``TradingModel.generate``,
     ``model.py:134-147``, obtains by recomputing the whole context).  16-bit
     inputs; query head h reads KV head h // repeats; repeats <= 8.
+
+    ``length`` is an int, or a one-element int32 tensor on the GPU that the
+    kernels read when they run (clamped to [1, capacity]): the launch then
+    covers the whole cache capacity and can be recorded once in a HIP graph
+    and replayed for every step.
     """
     if query.device.type != "cuda":
         raise RuntimeError("hip attention backend requires ROCm GPU tensors")
@@ -118,14 +123,46 @@ def decode_attention(
         raise ValueError(f"query heads must equal key/value heads multiplied by repeats (<= {MAX_DECODE_REPEATS})")
     if key_cache.shape[0] != query.shape[0] or key_cache.shape[3] != query.shape[3]:
         raise ValueError("query and caches must agree on batch and head_dim")
-    if not 1 <= length <= key_cache.shape[2]:
+    dev_length = isinstance(length, torch.Tensor)
+    if dev_length:
+        if length.dtype != torch.int32 or length.numel() != 1 or length.device != query.device:
+            raise ValueError("a tensor length must be a one-element int32 tensor on the query's device")
+    elif not 1 <= length <= key_cache.shape[2]:
         raise ValueError(f"length {length} outside [1, cache capacity {key_cache.shape[2]}]")
     if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
         raise RuntimeError("query and caches must share one dtype")
     if query.shape[-1] not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS} (got {query.shape[-1]})")
-    return torch.ops.mega_trading_amd.gqa_attn_decode(query, key_cache, value_cache, int(length),
-                                                      1.0 / math.sqrt(query.shape[-1]))
+    scale = 1.0 / math.sqrt(query.shape[-1])
+    if dev_length:
+        return torch.ops.mega_trading_amd.gqa_attn_decode_dev(query, key_cache, value_cache, length, scale)
+    return torch.ops.mega_trading_amd.gqa_attn_decode(query, key_cache, value_cache, int(length), scale)
+
+
+def decode_rope_append(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, cos: torch.Tensor,
+                       sin: torch.Tensor, pos, key_cache: torch.Tensor, value_cache: torch.Tensor) -> torch.Tensor:
+    """The decode step's RoPE and cache append in one launch: returns the
+    rotated query [B, Hq, 1, D] (cache dtype) and writes the rotated key and the
+    value of the new token into ``key_cache[:, :, pos]`` / ``value_cache[:, :, pos]``.
+    ``query`` [B, Hq, 1, D], ``key`` / ``value`` [B, Hkv, 1, D] (any float dtype:
+    fp32 is rounded to the cache dtype first, as the fused forward does);
+    ``cos`` / ``sin`` the fp32 RotaryEmbedding tables (row ``pos`` is used).
+    ``pos`` is an int or a one-element int32 GPU tensor read when the kernel
+    runs (clamped to the cache and table)."""
+    if key_cache.dtype not in _KERNEL_DTYPES or value_cache.dtype != key_cache.dtype:
+        raise RuntimeError("the caches must be float16 or bfloat16 and share one dtype")
+    if query.dtype not in (key_cache.dtype, torch.float32) or key.dtype != query.dtype or value.dtype != query.dtype:
+        raise RuntimeError("query, key and value must share one dtype: the cache dtype or float32")
+    last = min(key_cache.shape[2], cos.reshape(-1, cos.shape[-1]).shape[0]) - 1
+    if isinstance(pos, torch.Tensor):
+        if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != query.device:
+            raise ValueError("a tensor pos must be a one-element int32 tensor on the query's device")
+        return torch.ops.mega_trading_amd.decode_rope_append(query, key, value, cos, sin, last, pos, key_cache,
+                                                             value_cache)
+    if not 0 <= pos <= last:
+        raise ValueError(f"pos {pos} outside the cache / RoPE table")
+    return torch.ops.mega_trading_amd.decode_rope_append(query, key, value, cos, sin, int(pos), None, key_cache,
+                                                         value_cache)
 
 
 # ---------------------------------------------------------------------------
@@ -316,6 +353,61 @@ def gqa_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                                     torch.cuda.current_stream(q.device).cuda_stream)
     _native.check(rc, "mt_gqa_attn_decode")
     return out
+
+
+@torch.library.custom_op("mega_trading_amd::decode_rope_append", mutates_args=("k_cache", "v_cache"),
+                         device_types="cuda")
+def decode_rope_append_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                          pos: int, pos_dev: Optional[torch.Tensor], k_cache: torch.Tensor,
+                          v_cache: torch.Tensor) -> torch.Tensor:
+    import ctypes
+
+    lib = _native.load()
+    b, hq, _, d = q.shape
+    hkv = k.shape[1]
+    q_rot = torch.empty((b, hq, 1, d), device=q.device, dtype=k_cache.dtype)
+    cs = cos.reshape(-1, d // 2).contiguous()
+    sn = sin.reshape(-1, d // 2).contiguous()
+    ins = (ctypes.c_int64 * 6)(q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1))
+    cst = (ctypes.c_int64 * 6)(*k_cache.stride()[:3], *v_cache.stride()[:3])
+    in_dt = _native.DTYPE_FP32 if q.dtype == torch.float32 else _KERNEL_DTYPES[q.dtype]
+    with torch.cuda.device(q.device):
+        rc = lib.mt_decode_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), ins, cs.data_ptr(), sn.data_ptr(), pos,
+                                       _ptr(pos_dev), q_rot.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cst,
+                                       b, hq, hkv, d,
+                                       in_dt, _KERNEL_DTYPES[k_cache.dtype],
+                                       torch.cuda.current_stream(q.device).cuda_stream)
+    _native.check(rc, "mt_decode_rope_append")
+    return q_rot
+
+
+@decode_rope_append_op.register_fake
+def _decode_rope_append_fake(q, k, v, cos, sin, pos, pos_dev, k_cache, v_cache):
+    return q.new_empty(q.shape, dtype=k_cache.dtype)
+
+
+@torch.library.custom_op("mega_trading_amd::gqa_attn_decode_dev", mutates_args=(), device_types="cuda")
+def gqa_attn_decode_dev(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, length: torch.Tensor,
+                        scale: float) -> torch.Tensor:
+    lib = _native.load()
+    q, k_cache, v_cache = _kernel_ready(q), _kernel_ready(k_cache), _kernel_ready(v_cache)
+    b, hq, _, d = q.shape
+    hkv, cap = k_cache.shape[1], k_cache.shape[2]
+    out = torch.empty((b, hq, 1, d), device=q.device, dtype=q.dtype)
+    strides = _strides(q, k_cache, v_cache, out)
+    with torch.cuda.device(q.device):
+        ws_bytes = lib.mt_gqa_attn_decode_workspace_size(b, hq, cap, d)
+        ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
+        rc = lib.mt_gqa_attn_decode_dev(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), b, hq,
+                                        hkv, cap, length.data_ptr(), d, strides, scale, _KERNEL_DTYPES[q.dtype],
+                                        ws.data_ptr(), ws_bytes, torch.cuda.current_stream(q.device).cuda_stream)
+    _native.check(rc, "mt_gqa_attn_decode_dev")
+    return out
+
+
+@gqa_attn_decode_dev.register_fake
+def _gqa_attn_decode_dev_fake(q, k_cache, v_cache, length, scale):
+    return q.new_empty(q.shape)
 
 
 @gqa_attn_decode.register_fake

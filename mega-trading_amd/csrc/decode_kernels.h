@@ -27,9 +27,15 @@ struct DecodeParams {
   uint16_t* out;      // [B, Hq, 1, D]
   float* part;        // [B, Hq, nsplit, D + 2] fp32: o (unnormalised), m (log2), l
   int64_t sq[2], sk[3], sv[3], so[2];  // strides (b, h) for q / o, (b, h, t) for the caches
-  int B, Hq, Hkv, R, L, nsplit;
+  const int* length_dev;  // when set, L is read from device memory (graph-replayable decode)
+  int B, Hq, Hkv, R, L, nsplit;  // nsplit: splits in the grid (of the capacity when length_dev is set)
   float scale_log2;  // softmax scale * log2(e)
 };
+
+// With length_dev, L holds the capacity and the device value is clamped to [1, capacity].
+__device__ __forceinline__ int decode_length(const DecodeParams& p) {
+  return p.length_dev ? min(max(*p.length_dev, 1), p.L) : p.L;
+}
 
 template <class E, int D>
 __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) {
@@ -45,7 +51,9 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
   const int b = g / p.Hkv;
   const int R = p.R;
   const int k0 = s * kDecSplit;
-  const int n = min(kDecSplit, p.L - k0);
+  const int L = decode_length(p);
+  if (k0 >= L) return;  // a split past the current length (device-length launches cover the capacity)
+  const int n = min(kDecSplit, L - k0);
 
   for (int i = tid; i < R * D; i += 256) {
     const int h = i / D, d = i % D;
@@ -140,16 +148,83 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(DecodeParams p
   if (pair >= p.B * p.Hq) return;
   const int b = pair / p.Hq, h = pair % p.Hq;
   const float* src = p.part + (int64_t)pair * p.nsplit * (D + 2);
+  const int ns = (decode_length(p) + kDecSplit - 1) / kDecSplit;  // splits holding keys
   float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, src[s * (D + 2) + D]);
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, src[s * (D + 2) + D]);
   float o = 0.f, l = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
+  for (int s = 0; s < ns; ++s) {
     const float w = exp2_fast(src[s * (D + 2) + D] - M);
     o = __builtin_fmaf(w, src[s * (D + 2) + d], o);
     l = __builtin_fmaf(w, src[s * (D + 2) + D + 1], l);
   }
   const float r = o / l;
   p.out[b * p.so[0] + (int64_t)h * p.so[1] + d] = uint16_t(pack2<E>(r, 0.f) & 0xffffu);
+}
+
+// ---------------------------------------------------------------------------
+// The new token's RoPE and cache append, in one launch: q_rot = rot(q) (written
+// [B, Hq, 1, D]), k_cache[:, :, pos] = rot(k), v_cache[:, :, pos] = v.  The
+// inputs (views of the projections, [B, H, D] with strides (b, h), d stride 1)
+// are first rounded to the cache's 16-bit type, then rotated in fp32 with the
+// fp32 tables row `pos` and rounded again -- the sequence the fused forward
+// kernels apply to the prompt, so cached and recomputed keys are identical.
+// One thread per interleaved pair (x[2i], x[2i+1]).
+// ---------------------------------------------------------------------------
+struct RopeAppendParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t sq[2], sk[2], sv[2];
+  const float* cos;  // [>= pos + 1, D/2]
+  const float* sin;
+  uint16_t* q_out;   // [B, Hq, 1, D] contiguous
+  uint16_t* kc;      // [B, Hkv, cap, D] with strides (b, h, t)
+  uint16_t* vc;
+  int64_t skc[3], svc[3];
+  const int* pos_dev;  // when set, the position is read from device memory, clamped to [0, pos]
+  int B, Hq, Hkv, D, pos;
+};
+
+template <class E, int XT>
+__device__ __forceinline__ float load_in(const void* base, int64_t i) {
+  if constexpr (XT == 2) return E::to_f(uint16_t(pack2<E>(static_cast<const float*>(base)[i], 0.f) & 0xffffu));
+  else return E::to_f(static_cast<const uint16_t*>(base)[i]);
+}
+
+template <class E, int XT>
+__global__ __launch_bounds__(256) void decode_rope_append_kernel(RopeAppendParams p) {
+  const int half = p.D / 2;
+  const int pos = p.pos_dev ? min(max(*p.pos_dev, 0), p.pos) : p.pos;
+  const int64_t nq = (int64_t)p.B * p.Hq * half, nk = (int64_t)p.B * p.Hkv * half;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nq + 2 * nk) return;
+  if (i < nq + nk) {
+    const bool isq = i < nq;
+    const int64_t j = isq ? i : i - nq;
+    const int H = isq ? p.Hq : p.Hkv;
+    const int pr = int(j % half);
+    const int h = int((j / half) % H);
+    const int b = int(j / half / H);
+    const void* src = isq ? p.q : p.k;
+    const int64_t off = b * (isq ? p.sq[0] : p.sk[0]) + (int64_t)h * (isq ? p.sq[1] : p.sk[1]) + 2 * pr;
+    const float x0 = load_in<E, XT>(src, off), x1 = load_in<E, XT>(src, off + 1);
+    const float c = p.cos[(int64_t)pos * half + pr], sn = p.sin[(int64_t)pos * half + pr];
+    const uint32_t w = pack2<E>(x0 * c - x1 * sn, x0 * sn + x1 * c);
+    uint16_t* dst = isq ? p.q_out + ((int64_t)b * p.Hq + h) * p.D + 2 * pr
+                        : p.kc + b * p.skc[0] + (int64_t)h * p.skc[1] + (int64_t)pos * p.skc[2] + 2 * pr;
+    dst[0] = uint16_t(w & 0xffffu);
+    dst[1] = uint16_t(w >> 16);
+  } else {
+    const int64_t j = i - nq - nk;
+    const int pr = int(j % half);
+    const int h = int((j / half) % p.Hkv);
+    const int b = int(j / half / p.Hkv);
+    const int64_t off = b * p.sv[0] + (int64_t)h * p.sv[1] + 2 * pr;
+    const uint32_t w = pack2<E>(load_in<E, XT>(p.v, off), load_in<E, XT>(p.v, off + 1));
+    uint16_t* dst = p.vc + b * p.svc[0] + (int64_t)h * p.svc[1] + (int64_t)pos * p.svc[2] + 2 * pr;
+    dst[0] = uint16_t(w & 0xffffu);
+    dst[1] = uint16_t(w >> 16);
+  }
 }
 
 }  // namespace mt

@@ -337,9 +337,11 @@ size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D) {
   return ((size_t)B * Hq * nsplit * (D + 2) * sizeof(float) + 255) / 256 * 256;
 }
 
-int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv, int L,
-                       int D, const int64_t* strides, float scale, int dtype, void* workspace, size_t workspace_bytes,
-                       void* stream) {
+namespace {
+
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv, int L,
+                const int* length_dev, int D, const int64_t* strides, float scale, int dtype, void* workspace,
+                size_t workspace_bytes, void* stream) {
   int rc = check_common(B, Hq, Hkv, L, D, dtype, nullptr, nullptr);
   if (rc) return rc;
   if (Hq / Hkv > mt::kDecMaxR)
@@ -362,6 +364,7 @@ int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, 
   p.sk[0] = strides[4]; p.sk[1] = strides[5]; p.sk[2] = strides[6];
   p.sv[0] = strides[8]; p.sv[1] = strides[9]; p.sv[2] = strides[10];
   p.so[0] = strides[12]; p.so[1] = strides[13];
+  p.length_dev = length_dev;
   p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.R = Hq / Hkv; p.L = L;
   p.nsplit = (L + mt::kDecSplit - 1) / mt::kDecSplit;
   p.scale_log2 = scale * mt::kLog2e;
@@ -379,6 +382,61 @@ int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, 
 #undef MT_DECODE_LAUNCH
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "decode launch failed: %s", hipGetErrorString(e));
+}
+
+}  // namespace
+
+int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv, int L,
+                       int D, const int64_t* strides, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  return decode_impl(q, k_cache, v_cache, o, B, Hq, Hkv, L, nullptr, D, strides, scale, dtype, workspace,
+                     workspace_bytes, stream);
+}
+
+int mt_gqa_attn_decode_dev(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv,
+                           int capacity, const int* length_dev, int D, const int64_t* strides, float scale, int dtype,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (!length_dev) return fail(MT_E_NULL, "length_dev is NULL");
+  return decode_impl(q, k_cache, v_cache, o, B, Hq, Hkv, capacity, length_dev, D, strides, scale, dtype, workspace,
+                     workspace_bytes, stream);
+}
+
+int mt_decode_rope_append(const void* q, const void* k, const void* v, const int64_t* in_strides,
+                          const float* rope_cos, const float* rope_sin, int pos, const int* pos_dev, void* q_rot,
+                          void* k_cache, void* v_cache, const int64_t* cache_strides, int B, int Hq, int Hkv, int D,
+                          int in_dtype, int dtype, void* stream) {
+  int rc = check_common(B, Hq, Hkv, 1, D, dtype, rope_cos, rope_sin);
+  if (rc) return rc;
+  if (!q || !k || !v || !q_rot || !k_cache || !v_cache || !rope_cos || !in_strides || !cache_strides)
+    return fail(MT_E_NULL, "q, k, v, q_rot, k_cache, v_cache, rope tables and strides must be non-NULL");
+  if (in_dtype != MT_DTYPE_BF16 && in_dtype != MT_DTYPE_FP16 && in_dtype != 2)
+    return fail(MT_E_DTYPE, "input dtype code %d unsupported", in_dtype);
+  if (in_dtype != 2 && in_dtype != dtype) return fail(MT_E_DTYPE, "16-bit inputs must have the cache dtype");
+  if (pos < 0) return fail(MT_E_SHAPE, "pos must be >= 0 (got %d)", pos);
+  mt::RopeAppendParams p{};
+  p.q = q; p.k = k; p.v = v;
+  for (int i = 0; i < 2; ++i) {
+    p.sq[i] = in_strides[i]; p.sk[i] = in_strides[2 + i]; p.sv[i] = in_strides[4 + i];
+  }
+  for (int i = 0; i < 3; ++i) { p.skc[i] = cache_strides[i]; p.svc[i] = cache_strides[3 + i]; }
+  p.cos = rope_cos; p.sin = rope_sin;
+  p.q_out = static_cast<uint16_t*>(q_rot);
+  p.kc = static_cast<uint16_t*>(k_cache);
+  p.vc = static_cast<uint16_t*>(v_cache);
+  p.pos_dev = pos_dev;
+  p.B = B; p.Hq = Hq; p.Hkv = Hkv; p.D = D; p.pos = pos;
+  const int64_t n = (int64_t)B * (Hq + 2 * Hkv) * (D / 2);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+#define MT_RA(E, XT) hipLaunchKernelGGL((mt::decode_rope_append_kernel<E, XT>), grid, dim3(256), 0, st, p)
+  if (dtype == MT_DTYPE_BF16) {
+    if (in_dtype == 2) MT_RA(mt::BF16, 2); else MT_RA(mt::BF16, 0);
+  } else {
+    if (in_dtype == 2) MT_RA(mt::FP16, 2); else MT_RA(mt::FP16, 1);
+  }
+#undef MT_RA
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "rope append launch failed: %s", hipGetErrorString(e));
 }
 
 }  // extern "C"

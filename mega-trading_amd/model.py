@@ -38,6 +38,7 @@ from torch import nn
 from .attention import _rope_tables
 from .attention import attention as _hip_attention
 from .attention import decode_attention as _hip_decode_attention
+from .attention import decode_rope_append as _hip_decode_rope_append
 from .attention import rope_attention as _hip_rope_attention
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
 from .ops import rms_norm as _hip_rms_norm
@@ -103,6 +104,9 @@ class TradingModel(nn.Module):
         self.apply(_init_weights)
         self.output.weight = self.token_embedding.weight  # tied after init, as model.py:71
 
+    # KV-cached generate on the HIP routes replays one recorded HIP graph per token
+    decode_graphs = True
+
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         return self.output(self._hidden(input_ids))
 
@@ -145,14 +149,18 @@ class TradingModel(nn.Module):
         if self.operator_backend not in HIP_BACKENDS:
             return self._generate_recompute(input_ids, max_new_tokens, top_k)
         tokens = input_ids
-        cache = None
+        cache = step = None
         for _ in range(max_new_tokens):
             t = tokens.shape[1]
             if t > self.block_size:
-                cache = None
+                cache = step = None
                 logits = self(tokens[:, -self.block_size:])[:, -1, :]
             elif cache is None:
                 logits, cache = self._prefill(tokens)
+            elif self.decode_graphs:
+                if step is None:
+                    step = _DecodeGraph(self, cache, tokens.shape[0], tokens.device)
+                logits = step(tokens[:, -1:], t - 1)
             else:
                 logits = self._decode(tokens[:, -1:], cache, t - 1)
             tokens = torch.cat([tokens, _sample_next(logits, top_k)], dim=1)
@@ -179,11 +187,14 @@ class TradingModel(nn.Module):
             hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
         return self.output(self.norm(hidden))[:, -1, :], cache
 
-    def _decode(self, token: torch.Tensor, cache, pos: int) -> torch.Tensor:
-        """Logits after the token at position ``pos`` (its K/V are appended to the caches)."""
+    def _decode(self, token: torch.Tensor, cache, pos) -> torch.Tensor:
+        """Logits after the token at position ``pos`` (its K/V are appended to the
+        caches).  ``pos`` is an int, or a one-element int32 GPU tensor that the
+        kernels read when they run (the form a recorded HIP graph replays)."""
+        length = pos + 1
         hidden = self.token_embedding(token)
         for block, (k_cache, v_cache) in zip(self.blocks, cache):
-            hidden = hidden + block.attention.decode(block.attention_norm(hidden), k_cache, v_cache, pos)
+            hidden = hidden + block.attention.decode(block.attention_norm(hidden), k_cache, v_cache, pos, length)
             hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
         return self.output(self.norm(hidden))[:, -1, :]
 
@@ -312,19 +323,15 @@ class LlamaAttention(nn.Module):
         attended = out.to(hidden.dtype).transpose(1, 2).contiguous().view(b, t, hidden_dim)
         return self.o_proj(attended), k_cache, v_cache
 
-    def decode(self, hidden: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int) -> torch.Tensor:
-        """One token at position ``pos``: rotate its q/k (fp32 from the 16-bit
-        values, as the fused kernels do), append k/v to the caches, attend."""
+    def decode(self, hidden: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos, length=None):
+        """One token at position ``pos`` (int or device int32 tensor): rotate its
+        q/k (fp32 from the 16-bit values, as the fused kernels do), append k/v to
+        the caches, attend over positions 0..pos."""
         b, _, hidden_dim = hidden.shape
         query, key, value = self._heads(hidden)
-        kdt = k_cache.dtype
-        cos = self.rope.cos[0, 0, pos:pos + 1]
-        sin = self.rope.sin[0, 0, pos:pos + 1]
-        q_rot = rotate(query.to(kdt).float(), cos, sin).to(kdt)
-        k_rot = rotate(key.to(kdt).float(), cos, sin).to(kdt)
-        k_cache[:, :, pos] = k_rot[:, :, 0]
-        v_cache[:, :, pos] = value[:, :, 0].to(kdt)
-        out = _hip_decode_attention(q_rot, k_cache, v_cache, pos + 1, repeats=self.repeats)
+        q_rot = _hip_decode_rope_append(query, key, value, self.rope.cos, self.rope.sin, pos, k_cache, v_cache)
+        out = _hip_decode_attention(q_rot, k_cache, v_cache, pos + 1 if length is None else length,
+                                    repeats=self.repeats)
         attended = out.to(hidden.dtype).transpose(1, 2).reshape(b, 1, hidden_dim)
         return self.o_proj(attended)
 
@@ -390,6 +397,41 @@ class RotaryEmbedding(nn.Module):
         cos = self.cos[:, :, :sequence_length].to(dtype=query.dtype)
         sin = self.sin[:, :, :sequence_length].to(dtype=query.dtype)
         return rotate(query, cos, sin), rotate(key, cos, sin)
+
+
+class _DecodeGraph:
+    """One decode step of ``TradingModel._decode`` recorded as a HIP graph and
+    replayed for every new token.  The token and its position live in device
+    buffers that the recorded kernels read (the decode kernels take the length
+    from device memory and cover the cache capacity), so one recording serves
+    every position; the host only writes the next token and position before
+    each replay.  Replaying a step again for the same position rewrites the
+    same cache row with the same values, so the first call (warm-up, record,
+    replay) is harmless.  The returned logits are the graph's static buffer,
+    valid until the next call."""
+
+    def __init__(self, model: "TradingModel", cache, batch: int, device: torch.device):
+        self.model = model
+        self.cache = cache
+        self.tok = torch.zeros((batch, 1), dtype=torch.long, device=device)
+        self.pos = torch.zeros((1,), dtype=torch.int32, device=device)
+        self.graph = None
+        self.out = None
+
+    def __call__(self, token: torch.Tensor, pos: int) -> torch.Tensor:
+        self.tok.copy_(token)
+        self.pos.fill_(pos)
+        if self.graph is None:
+            side = torch.cuda.Stream(device=self.tok.device)
+            side.wait_stream(torch.cuda.current_stream(self.tok.device))
+            with torch.cuda.stream(side):  # warm-up: allocator and library state outside the recording
+                self.model._decode(self.tok, self.cache, self.pos)
+            torch.cuda.current_stream(self.tok.device).wait_stream(side)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.out = self.model._decode(self.tok, self.cache, self.pos)
+        self.graph.replay()
+        return self.out
 
 
 def _sample_next(logits: torch.Tensor, top_k: int) -> torch.Tensor:

@@ -119,3 +119,58 @@ def test_generate_sampling_runs_at_c5_shape():
     torch.manual_seed(0)
     out = m.generate(ids.cuda(), max_new_tokens=16, top_k=16)
     assert out.shape == (8, 272) and int(out.max()) < wl.C5_MODEL["vocab_size"] and int(out.min()) >= 0
+
+
+@pytest.mark.parametrize("in_dt", [torch.float32, torch.bfloat16])
+def test_decode_rope_append_matches_torch_rotation(in_dt):
+    attn = importlib.import_module("mega-trading_amd.attention")
+    g = torch.Generator().manual_seed(21)
+    b, hq, hkv, d, cap, pos = 3, 8, 2, 64, 40, 17
+    proj_q = torch.randn(b, 1, hq * d, generator=g).to(in_dt).cuda()
+    proj_kv = torch.randn(b, 1, 2 * hkv * d, generator=g).to(in_dt).cuda()
+    q = proj_q.view(b, 1, hq, d).transpose(1, 2)               # strided views, as the model passes them
+    k = proj_kv[..., : hkv * d].view(b, 1, hkv, d).transpose(1, 2)
+    v = proj_kv[..., hkv * d:].view(b, 1, hkv, d).transpose(1, 2)
+    rope = model_mod.RotaryEmbedding(d, 64, theta=10_000.0).cuda()
+    kc = torch.zeros(b, hkv, cap, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    q_rot = attn.decode_rope_append(q, k, v, rope.cos, rope.sin, pos, kc, vc)
+    c, s = rope.cos[0, 0, pos:pos + 1], rope.sin[0, 0, pos:pos + 1]
+    ref_q = model_mod.rotate(q.to(torch.bfloat16).float(), c, s).to(torch.bfloat16)
+    ref_k = model_mod.rotate(k.to(torch.bfloat16).float(), c, s).to(torch.bfloat16)
+    for got, ref in ((q_rot, ref_q), (kc[:, :, pos:pos + 1], ref_k)):
+        assert float((got == ref).float().mean()) > 0.99  # last-ulp fp32 differences may flip a rounding
+        torch.testing.assert_close(got.float(), ref.float(), rtol=2 ** -7, atol=1e-6)
+    assert torch.equal(vc[:, :, pos], v[:, :, 0].to(torch.bfloat16))
+    assert not kc[:, :, :pos].any() and not kc[:, :, pos + 1:].any()  # only row pos written
+
+
+def test_graph_decode_replays_match_eager_decode():
+    # one recorded decode step, replayed per position (device-side token and position), against
+    # the eager step with a host position, token for token, with eager work between the replays
+    m = _model("hip")
+    g = torch.Generator().manual_seed(31)
+    tokens = torch.randint(0, 128, (4, 30), generator=g).cuda()
+    with torch.no_grad():
+        _, cache_a = m._prefill(tokens[:, :12])
+        cache_b = [(k.clone(), v.clone()) for k, v in cache_a]
+        step = model_mod._DecodeGraph(m, cache_b, 4, tokens.device)
+        for pos in range(12, 30):
+            eager = m._decode(tokens[:, pos:pos + 1], cache_a, pos)
+            torch.cuda.synchronize()
+            replay = step(tokens[:, pos:pos + 1], pos).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(replay, eager), pos
+        for (ka, va), (kb, vb) in zip(cache_a, cache_b):
+            assert torch.equal(ka[:, :, :30], kb[:, :, :30]) and torch.equal(va[:, :, :30], vb[:, :, :30])
+
+
+def test_generate_with_graphs_equals_without():
+    m = _model("hip", block_size=48)
+    g = torch.Generator().manual_seed(32)
+    prompt = torch.randint(0, 128, (3, 10), generator=g).cuda()
+    m.decode_graphs = False
+    a = m.generate(prompt, max_new_tokens=45, top_k=1)  # crosses block_size 48 at the end
+    m.decode_graphs = True
+    b = m.generate(prompt, max_new_tokens=45, top_k=1)
+    assert torch.equal(a, b)
