@@ -50,8 +50,8 @@ struct AttnParams {
   uint16_t* dk;
   uint16_t* dv;
   float* lse;      // [B, Hq, T] natural-log LSE (written by fwd, read by bwd)
-  float* delta;    // [B, Hq, T] rowsum(O * dO) workspace (bwd)
-  float* lse2;     // [B, Hq, T] LSE * log2(e) workspace (written by dQ, read by dK/dV)
+  float* ndelta;   // [B, Hq, T] -rowsum(O * dO) workspace (written by dQ, read by dK/dV)
+  float* nlse2;    // [B, Hq, T] -LSE * log2(e) workspace (written by dQ, read by dK/dV)
   float* part;     // [n_split, 2, B, Hkv, T, D] fp32 dK/dV partial sums (bwd, n_split > 1)
   const float* cos;  // [T, D/2] fp32 or null
   const float* sin;
@@ -582,9 +582,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
       dsum = sum_with_partner(dsum);
       dlt[nt] = dsum;
       lse2[nt] = ok ? lx[nt] * kLog2e : 0.f;
-      if (ok && hh == 0) {
-        p.delta[rowbase + row] = dsum;
-        p.lse2[rowbase + row] = lse2[nt];
+      if (ok && hh == 0) {  // negated: the dK/dV pass seeds its accumulators with them
+        p.ndelta[rowbase + row] = -dsum;
+        p.nlse2[rowbase + row] = -lse2[nt];
       }
     }
   }
@@ -649,35 +649,43 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
 
 
 // dK/dV softmax step for one 32-row quarter (C layout: lane = key, slots =
-// rows): P = 2^(S*c - lse2[row]), dS = P * (dP - delta[row]); packs P and dS
-// into the two 16-row B operands.  l_rows / d_rows point at the quarter's
-// lse2 / delta values offset by 4 * (lane / 32); slot group g reads rows
-// 8g .. 8g+3.  With MASK, entries whose key exceeds the row or whose row is
-// at or past T are zeroed (qrow = the quarter's first global row).
+// rows).  The score MFMAs start from the accumulator tiles -lse2[row] and
+// -delta[row] (see dkv_step) with K pre-scaled by scale*log2(e), so on entry
+// s = S*c - lse2 and dp = dP - delta; this computes P = 2^s, dS = P * dp and
+// packs both into the two 16-row B operands.  With MASK, entries whose key
+// exceeds the row or whose row is at or past T are zeroed (qrow = the
+// quarter's first global row).
 template <class E, bool MASK>
-__device__ __forceinline__ void softmax_dS32(f32x16& s, f32x16& dp, const float* l_rows, const float* d_rows,
-                                             float c2, int key, int qrow, int T, int hh,
+__device__ __forceinline__ void softmax_dS32(f32x16& s, f32x16& dp, int key, int qrow, int T, int hh,
                                              typename E::v8 pk[2], typename E::v8 dk[2]) {
 #pragma unroll
-  for (int g4 = 0; g4 < 4; ++g4) {
-    const f32x4 l4 = *reinterpret_cast<const f32x4*>(l_rows + 8 * g4);
-    const f32x4 d4 = *reinterpret_cast<const f32x4*>(d_rows + 8 * g4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 4 * g4 + e;
-      float pv = exp2_fast(__builtin_fmaf(s[i], c2, -l4[e]));
-      if constexpr (MASK) {
-        const int qg = qrow + 8 * g4 + 4 * hh + e;
-        if (key > qg || qg >= T) pv = 0.f;
-      }
-      s[i] = pv;
-      dp[i] = pv * (dp[i] - d4[e]);
+  for (int i = 0; i < 16; ++i) {
+    float pv = exp2_fast(s[i]);
+    if constexpr (MASK) {
+      const int qg = qrow + 8 * (i >> 2) + 4 * hh + (i & 3);
+      if (key > qg || qg >= T) pv = 0.f;
     }
+    s[i] = pv;
+    dp[i] = pv * dp[i];
   }
   pk[0] = pack8<E>(s, 0);
   pk[1] = pack8<E>(s, 8);
   dk[0] = pack8<E>(dp, 0);
   dk[1] = pack8<E>(dp, 8);
+}
+
+// The 16 accumulator slots of a 32-row quarter (slot i = row 8(i/4) + 4(lane/32)
+// + i%4) filled from a row-indexed fp32 vector in LDS; `rows` already points at
+// the quarter's first row plus 4 * (lane / 32).
+__device__ __forceinline__ f32x16 row_tile(const float* rows) {
+  f32x16 t;
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(rows + 8 * g4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[4 * g4 + e] = v[e];
+  }
+  return t;
 }
 
 // ===========================================================================
@@ -708,7 +716,7 @@ template <class E, int D, bool MASK>
 __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const float* lrow, const float* drow,
                                          const typename E::v8* kop, const typename E::v8* vop,
                                          f32x16* dkacc, f32x16* dvacc, int rbase, TrBase tbase, int lane,
-                                         int key, int k0, int qrow0, int T, float c2) {
+                                         int key, int k0, int qrow0, int T) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
@@ -725,8 +733,9 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
     const int r0 = 32 * (h & 1);
     V8 aq = TL::template row_op<E>(Qh, rbase, r0, 0);
     V8 ag = TL::template row_op<E>(Gh, rbase, r0, 0);
-    s = E::mfma(aq, kop[0], f32x16{});
-    dp = E::mfma(ag, vop[0], f32x16{});
+    // accumulators start at -lse2 / -delta of the quarter's rows
+    s = E::mfma(aq, kop[0], row_tile(lrow + 32 * h + 4 * hh));
+    dp = E::mfma(ag, vop[0], row_tile(drow + 32 * h + 4 * hh));
 #pragma unroll
     for (int kk = 1; kk < KT; ++kk) {
       aq = TL::template row_op<E>(Qh, rbase, r0, kk);
@@ -736,7 +745,7 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
     }
   };
   auto vh = [&](int h, f32x16& s, f32x16& dp, V8* pk, V8* dk) {
-    softmax_dS32<E, MASK>(s, dp, lrow + 32 * h + 4 * hh, drow + 32 * h + 4 * hh, c2, key, qrow0 + 32 * h, T, hh, pk, dk);
+    softmax_dS32<E, MASK>(s, dp, key, qrow0 + 32 * h, T, hh, pk, dk);
   };
   auto dvdk = [&](int h, const V8* pk, const V8* dk) {
     const char* Qh = Q + (h >> 1) * TL::BYTES;
@@ -821,7 +830,7 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   constexpr int DT = D / 32;
   // [buf][Q, dO] x 128 rows (two 64-row tiles back to back)
   __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];
-  __shared__ __attribute__((aligned(16))) float vec[2][2][kKvRows];  // [buf][lse * log2(e), delta]
+  __shared__ __attribute__((aligned(16))) float vec[2][2][kKvRows];  // [buf][-lse * log2(e), -delta]
 
   // heaviest key blocks (smallest index: most causal rows) first
   const int groups = p.B * p.Hkv * p.n_split;
@@ -842,16 +851,26 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   const int key = k0 + l32;                      // this lane's key (C column)
   const bool wave_live = k0 < p.T;
 
-  // K and V rows as B operands (N = key, k = d)
+  // K and V rows as B operands (N = key, k = d).  K is pre-multiplied by
+  // scale * log2(e) (rounded to the storage type once), so the score MFMA
+  // yields S * c directly and the softmax needs no per-score multiply.
   V8 kop[KT], vop[KT];
   {
     const uint16_t* kbase = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1];
     const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1];
+    u32x4 kx[KT];
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
       const int d0 = 16 * kk + 8 * hh;
-      kop[kk] = __builtin_bit_cast(V8, load_chunk(kbase, p.sk[2], key, p.T, d0));
+      kx[kk] = load_chunk(kbase, p.sk[2], key, p.T, d0);
       vop[kk] = __builtin_bit_cast(V8, load_chunk(vbase, p.sv[2], key, p.T, d0));
+    }
+    const float c2 = p.scale_log2;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) kx[kk][w] = pack2<E>(lo_f<E>(kx[kk][w]) * c2, hi_f<E>(kx[kk][w]) * c2);
+      kop[kk] = __builtin_bit_cast(V8, kx[kk]);
     }
   }
 
@@ -881,7 +900,7 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
     qs_stage.stage(smem[buf][0] + TL::BYTES, qh, p.sq[2], row0 + kBlk, p.T);
     gs_stage.stage(smem[buf][1] + TL::BYTES, gh, p.sdo[2], row0 + kBlk, p.T);
     const int64_t rb = ((int64_t)b * p.Hq + head) * p.T;
-    const float* src = (wave & 2) ? p.delta + rb : p.lse2 + rb;
+    const float* src = (wave & 2) ? p.ndelta + rb : p.nlse2 + rb;
     stage_vec64(reinterpret_cast<char*>(&vec[buf][wave >> 1][(wave & 1) * kBlk]), src, row0 + (wave & 1) * kBlk, p.T, lane);
   };
 
@@ -889,7 +908,6 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
   stage(nxt_head, nxt_row, 0);
   wait_vmem();
   __syncthreads();
-  const float c2 = p.scale_log2;
   for (int it = 0; it < n_it; ++it) {
     const int buf = it & 1;
     cur_row = nxt_row;
@@ -904,10 +922,10 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
       const bool fast = (k0 + kKvKpw - 1 <= cur_row) && (cur_row + kKvRows <= p.T);
       if (fast)
         dkv_step<E, D, false>(smem[buf][0], smem[buf][1], vec[buf][0], vec[buf][1], kop, vop, dkacc, dvacc,
-                              rbase_op, tbase_op, lane, key, k0, cur_row, p.T, c2);
+                              rbase_op, tbase_op, lane, key, k0, cur_row, p.T);
       else
         dkv_step<E, D, true>(smem[buf][0], smem[buf][1], vec[buf][0], vec[buf][1], kop, vop, dkacc, dvacc,
-                             rbase_op, tbase_op, lane, key, k0, cur_row, p.T, c2);
+                             rbase_op, tbase_op, lane, key, k0, cur_row, p.T);
     }
     wait_vmem();
     __syncthreads();

@@ -114,7 +114,7 @@ int choose_split(int B, int Hq, int Hkv, int T, int D) {
   return split;
 }
 
-// workspace layout: delta [B,Hq,T] fp32 | lse*log2(e) [B,Hq,T] fp32 | dK/dV partials
+// workspace layout: -delta [B,Hq,T] fp32 | -lse*log2(e) [B,Hq,T] fp32 | dK/dV partials
 size_t vec_bytes(int B, int Hq, int T) { return (((size_t)B * Hq * T * sizeof(float)) + 255) / 256 * 256; }
 size_t delta_bytes(int B, int Hq, int T) { return 2 * vec_bytes(B, Hq, T); }
 
@@ -240,8 +240,8 @@ int bwd_impl(int stage, const void* q, const void* k, const void* v, const void*
   p.dk = static_cast<uint16_t*>(dk);
   p.dv = static_cast<uint16_t*>(dv);
   p.lse = const_cast<float*>(lse);
-  p.delta = static_cast<float*>(workspace);
-  p.lse2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vec_bytes(B, Hq, T));
+  p.ndelta = static_cast<float*>(workspace);
+  p.nlse2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vec_bytes(B, Hq, T));
   p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + delta_bytes(B, Hq, T));
   p.cos = rope_cos;
   p.sin = rope_sin;
