@@ -457,6 +457,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
 // One 64-key K/V tile against the wave's 64 query rows: S^T and dP^T
 // recomputed (lane = query), P = 2^(S c2 - lse2), dS = P (dP - delta),
 // dQ += dS K.  With MASK (the diagonal tile) keys above the query get P = 0.
+// For D <= 64 the two 32-key halves mt run one after the other and each K / V
+// operand read from LDS (row reads for S^T / dP^T, transposed reads for dQ)
+// feeds both 32-query halves nt of the wave.
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typename E::v8 (*qop)[D / 16],
                                         const typename E::v8 (*gop)[D / 16], f32x16 (*dqacc)[2], const float* lse2,
@@ -465,51 +468,93 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  // the two 32-query halves one after the other keeps S/dP at 64 VGPRs
+  if constexpr (D > 64) {
+    // D = 128: query halves outer (each re-reads the K / V operands), which
+    // keeps the one-wave-per-SIMD working set within the registers
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    f32x16 st[2], dpt[2];
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x16 st[2], dpt[2];  // [mt]
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      {
-        const V8 a = TL::template row_op<E>(K, rbase, mt * 32, 0);
-        const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
-        st[mt] = E::mfma(a, qop[nt][0], f32x16{});
-        dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
+      for (int mt = 0; mt < 2; ++mt) {
+        st[mt] = E::mfma(TL::template row_op<E>(K, rbase, mt * 32, 0), qop[nt][0], f32x16{});
+        dpt[mt] = E::mfma(TL::template row_op<E>(Vr, rbase, mt * 32, 0), gop[nt][0], f32x16{});
+#pragma unroll
+        for (int kk = 1; kk < KT; ++kk) {
+          st[mt] = E::mfma(TL::template row_op<E>(K, rbase, mt * 32, kk), qop[nt][kk], st[mt]);
+          dpt[mt] = E::mfma(TL::template row_op<E>(Vr, rbase, mt * 32, kk), gop[nt][kk], dpt[mt]);
+        }
       }
 #pragma unroll
-      for (int kk = 1; kk < KT; ++kk) {
-        const V8 a = TL::template row_op<E>(K, rbase, mt * 32, kk);
-        const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, kk);
-        st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
-        dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
+      for (int mt = 0; mt < 2; ++mt) {
+        V8 dsb[2];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
+          if constexpr (MASK) {
+            const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+            if (kr > nt * 32 + l32) pv = 0.f;
+          }
+          st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
+        }
+        dsb[0] = pack8<E>(st[mt], 0);
+        dsb[1] = pack8<E>(st[mt], 8);
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+            dqacc[dt][nt] = E::mfma(TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt), dsb[k2], dqacc[dt][nt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    f32x16 st[2], dpt[2];  // [nt]
+    {
+      const V8 a = TL::template row_op<E>(K, rbase, mt * 32, 0);
+      const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        st[nt] = E::mfma(a, qop[nt][0], f32x16{});
+        dpt[nt] = E::mfma(b, gop[nt][0], f32x16{});
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      V8 dsb[2];
+    for (int kk = 1; kk < KT; ++kk) {
+      const V8 a = TL::template row_op<E>(K, rbase, mt * 32, kk);
+      const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, kk);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        st[nt] = E::mfma(a, qop[nt][kk], st[nt]);
+        dpt[nt] = E::mfma(b, gop[nt][kk], dpt[nt]);
+      }
+    }
+    V8 dsb[2][2];  // [nt][k2]
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
+        float pv = exp2_fast(__builtin_fmaf(st[nt][i], c2, -lse2[nt]));
         if constexpr (MASK) {
           const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
           if (kr > nt * 32 + l32) pv = 0.f;
         }
-        st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
+        st[nt][i] = pv * (dpt[nt][i] - dlt[nt]);
       }
-      dsb[0] = pack8<E>(st[mt], 0);
-      dsb[1] = pack8<E>(st[mt], 8);
+      dsb[nt][0] = pack8<E>(st[nt], 0);
+      dsb[nt][1] = pack8<E>(st[nt], 8);
+    }
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
+    for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const V8 a = TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt);
-          dqacc[dt][nt] = E::mfma(a, dsb[k2], dqacc[dt][nt]);
-        }
+      for (int dt = 0; dt < DT; ++dt) {
+        const V8 a = TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) dqacc[dt][nt] = E::mfma(a, dsb[nt][k2], dqacc[dt][nt]);
       }
     }
-    // keep the two halves' live ranges apart (the scheduler would
-    // otherwise interleave them and exceed the register budget)
+    // keep the two halves' live ranges apart
     __builtin_amdgcn_sched_barrier(0);
   }
 }
