@@ -452,6 +452,227 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnPara
 }
 
 // ===========================================================================
+// Forward for D = 128: 8 waves of 32 query rows per workgroup
+// ===========================================================================
+// At D = 128 the 64-row waves of attn_fwd_kernel need one SIMD each and spill.
+// Here a workgroup is 8 waves: the 4 (head, 64-row block) pairs of a RowTask
+// split into two 32-row waves, two waves per SIMD, so each staged 128-key K/V
+// tile still feeds 256 query rows and no wave spills.  The softmax is that of
+// attn_fwd_kernel (fp32 scale and offset per score, lazy rescaling).
+constexpr int kFwdW8Waves = 8;
+
+template <class E, int D, bool MASK>
+__device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const typename E::v8* qop, f32x16* oacc,
+                                           float& mrun, float& lrun, int rbase, TrBase tbase, int lane, int kt0,
+                                           int q0, float c2) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+  const int hh = lane >> 5;
+  const int l32 = lane & 31;
+  bool live[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) live[h] = !MASK || (kt0 + 32 * h <= q0 + 31);
+
+  auto sq = [&](int h, f32x16& st) {
+    const char* Kh = K + (h >> 1) * TL::BYTES;
+    const int r0 = 32 * (h & 1);
+    st = E::mfma(TL::template row_op<E>(Kh, rbase, r0, 0), qop[0], f32x16{});
+#pragma unroll
+    for (int kk = 1; kk < KT; ++kk) st = E::mfma(TL::template row_op<E>(Kh, rbase, r0, kk), qop[kk], st);
+  };
+  // P = 2^(s*c - m) packed to 16 bits (the scores kept for a possible
+  // rescale); returns this lane's share of the quarter's row sum
+  auto ex = [&](int h, f32x16& st, V8* pk) {
+    if constexpr (MASK) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kr = kt0 + 32 * h + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (kr > q0 + l32) st[i] = -INFINITY;
+      }
+    }
+    const float moff = mrun;
+    u32x4 w[2];
+#pragma unroll
+    for (int p2 = 0; p2 < 8; ++p2)
+      w[p2 >> 2][p2 & 3] = pack2<E>(exp2_fast(__builtin_fmaf(st[2 * p2], c2, -moff)),
+                                    exp2_fast(__builtin_fmaf(st[2 * p2 + 1], c2, -moff)));
+    float s0 = E::sum2(w[0][0], 0.f), s1 = E::sum2(w[1][0], 0.f);
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      s0 = E::sum2(w[0][q], s0);
+      s1 = E::sum2(w[1][q], s1);
+    }
+    pk[0] = __builtin_bit_cast(V8, w[0]);
+    pk[1] = __builtin_bit_cast(V8, w[1]);
+    return s0 + s1;
+  };
+  // overflow test (the first quarter, m = -inf, fails it by construction); on
+  // failure raise m to the row max, rescale O and l and redo E
+  auto chk = [&](int h, f32x16& st, V8* pk, float qs) {
+    if (__builtin_amdgcn_ballot_w64(!(qs <= kSumLimit))) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v = fmaxf(v, st[i]);
+      const float mnew = fmaxf(mrun, max_with_partner(v) * c2);
+      const float alpha = exp2_fast(mrun - mnew);
+      mrun = mnew;
+      lrun *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+      qs = ex(h, st, pk);
+    }
+    lrun += qs;
+  };
+  auto pv = [&](int h, const V8* pk) {
+    const char* Vh = Vt + (h >> 1) * TL::BYTES;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        oacc[dt] = E::mfma(TL::template tr_op<E>(Vh, tbase, 2 * (h & 1) + k2, dt), pk[k2], oacc[dt]);
+  };
+
+  // S(h+1) is issued before E(h) so the score MFMAs overlap the softmax
+  f32x16 st[2];
+  V8 pk[2];
+  if (live[0]) sq(0, st[0]);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    if (h < 3 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
+    float qs = 0.f;
+    if (live[h]) qs = ex(h, st[h & 1], pk);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live[h]) {
+      chk(h, st[h & 1], pk, qs);
+      pv(h, pk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <class E, int D, bool ROPE, bool PEEL>
+__global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnParams p) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int SW = TL::INSTR < kFwdW8Waves ? TL::INSTR : kFwdW8Waves;  // waves that stage tiles
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];  // [buf][K, V] x 128 rows
+
+  const RowTask task = row_task(p);
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const int pw = wave >> 1;                         // (head, row block) pair of this wave
+  const int head = task.kvh * p.R + task.hs * p.r_sub + (pw % p.r_sub);
+  const int qb = task.sb * p.rb + pw / p.r_sub;     // this wave's row block
+  const int q0 = qb * kBlk + 32 * (wave & 1);       // this wave's first row
+  const bool active = qb < p.nqb && q0 < p.T;
+  const int jw = (q0 + 31) / kFwdKeys;              // this wave's diagonal tile
+  const int last_row = min(p.T, (task.sb * p.rb + p.rb) * kBlk) - 1;
+  const int jlast = last_row / kFwdKeys;
+
+  const uint16_t* kbase = p.k + task.b * p.sk[0] + (int64_t)task.kvh * p.sk[1];
+  const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
+
+  // Q^T as B operands, rotated if RoPE (and written out); rows past T load
+  // row T-1 and are zeroed
+  V8 qop[KT];
+  {
+    const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
+    uint16_t* rbase = ROPE ? p.qrot + ((int64_t)task.b * p.Hq + head) * p.T * D : nullptr;
+    const int row = q0 + l32;
+    const int rc = min(row, p.T - 1);
+    const bool ok = active && row < p.T;
+    u32x4 x[KT];
+    f32x4 cs[ROPE ? KT : 1], sn[ROPE ? KT : 1];
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      const int d0 = 16 * kk + 8 * hh;
+      x[kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
+      if constexpr (ROPE) load_rope_cs<D>(p.cos, p.sin, rc, d0, cs[kk], sn[kk]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      const int d0 = 16 * kk + 8 * hh;
+      u32x4 y = ok ? x[kk] : zero4();
+      if constexpr (ROPE) {
+        y = rope_chunk<E>(y, cs[kk], sn[kk]);
+        if (ok) *reinterpret_cast<u32x4*>(rbase + (int64_t)row * D + d0) = y;
+      }
+      qop[kk] = __builtin_bit_cast(V8, y);
+    }
+  }
+
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) zero16(oacc[dt]);
+  float mrun = -INFINITY;
+  float lrun = 0.f;
+  const float c2 = p.scale_log2;
+
+  Stager<D, SW> ks_stage, vs_stage;
+  const bool stager = wave < SW;
+  ks_stage.init(p.sk[2], wave, lane);
+  vs_stage.init(p.sv[2], wave, lane);
+  const int rbase_op = TL::row_base(lane);
+  const TrBase tbase_op = TL::tr_base(lane);
+  auto stage = [&](int j, int buf) {
+    if (!stager) return;
+    const int r0 = j * kFwdKeys;
+    ks_stage.stage(smem[buf][0], kbase, p.sk[2], r0, p.T);
+    vs_stage.stage(smem[buf][1], vbase, p.sv[2], r0, p.T);
+    ks_stage.stage(smem[buf][0] + TL::BYTES, kbase, p.sk[2], r0 + kBlk, p.T);
+    vs_stage.stage(smem[buf][1] + TL::BYTES, vbase, p.sv[2], r0 + kBlk, p.T);
+  };
+
+  stage(0, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
+    const int buf = j & 1;
+    if (j < jlast) stage(j + 1, buf ^ 1);
+    if (active && j <= jw) {
+      if (PEEL || j < jw)
+        fwd32_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                                j * kFwdKeys, q0, c2);
+      else
+        fwd32_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                               j * kFwdKeys, q0, c2);
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+  if (PEEL && active)  // jw == jlast
+    fwd32_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, oacc, mrun, lrun, rbase_op, tbase_op,
+                           lane, jlast * kFwdKeys, q0, c2);
+
+  if (!active) return;
+  const int row = q0 + l32;
+  if (row >= p.T) return;
+  uint16_t* obase = p.out + task.b * p.so[0] + (int64_t)head * p.so[1];
+  float* lbase = p.lse + ((int64_t)task.b * p.Hq + head) * p.T;
+  const float lt = sum_with_partner(lrun);
+  const float inv = 1.f / lt;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = dt * 32 + 8 * g + 4 * hh;
+      u32x2 w = {pack2<E>(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv),
+                 pack2<E>(oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv)};
+      *reinterpret_cast<u32x2*>(obase + (int64_t)row * p.so[2] + d) = w;
+    }
+  if (hh == 0) lbase[row] = (mrun + __builtin_amdgcn_logf(lt)) * kLn2;
+}
+
+// ===========================================================================
 // Backward, dQ (also writes delta = rowsum(O * dO))
 // ===========================================================================
 // One 64-key K/V tile against the wave's 64 query rows: S^T and dP^T
@@ -476,12 +697,18 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
       f32x16 st[2], dpt[2];  // [mt]
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        st[mt] = E::mfma(TL::template row_op<E>(K, rbase, mt * 32, 0), qop[nt][0], f32x16{});
-        dpt[mt] = E::mfma(TL::template row_op<E>(Vr, rbase, mt * 32, 0), gop[nt][0], f32x16{});
+        {
+          const V8 a = TL::template row_op<E>(K, rbase, mt * 32, 0);
+          const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
+          st[mt] = E::mfma(a, qop[nt][0], f32x16{});
+          dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
+        }
 #pragma unroll
         for (int kk = 1; kk < KT; ++kk) {
-          st[mt] = E::mfma(TL::template row_op<E>(K, rbase, mt * 32, kk), qop[nt][kk], st[mt]);
-          dpt[mt] = E::mfma(TL::template row_op<E>(Vr, rbase, mt * 32, kk), gop[nt][kk], dpt[mt]);
+          const V8 a = TL::template row_op<E>(K, rbase, mt * 32, kk);
+          const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, kk);
+          st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
+          dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
         }
       }
 #pragma unroll
@@ -499,11 +726,16 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
         dsb[0] = pack8<E>(st[mt], 0);
         dsb[1] = pack8<E>(st[mt], 8);
 #pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2)
+        for (int k2 = 0; k2 < 2; ++k2) {
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            dqacc[dt][nt] = E::mfma(TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt), dsb[k2], dqacc[dt][nt]);
+          for (int dt = 0; dt < DT; ++dt) {
+            const V8 a = TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt);
+            dqacc[dt][nt] = E::mfma(a, dsb[k2], dqacc[dt][nt]);
+          }
+        }
       }
+      // keep the two halves' live ranges apart (the scheduler would
+      // otherwise interleave them and exceed the register budget)
       __builtin_amdgcn_sched_barrier(0);
     }
     return;

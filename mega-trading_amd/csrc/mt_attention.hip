@@ -162,8 +162,14 @@ hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
     p.sk[2] = D;
   }
   dim3 grid(p.nsb * p.B * p.Hkv * p.n_hsub);
-  return p.rb == 1 ? launch_main(mt::attn_fwd_kernel<E, D, ROPE, true>, grid, dim3(256), st, p)
-                   : launch_main(mt::attn_fwd_kernel<E, D, ROPE, false>, grid, dim3(256), st, p);
+  if constexpr (D > 64) {
+    const dim3 block(64 * mt::kFwdW8Waves);
+    return p.rb == 1 ? launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, true>, grid, block, st, p)
+                     : launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, false>, grid, block, st, p);
+  } else {
+    return p.rb == 1 ? launch_main(mt::attn_fwd_kernel<E, D, ROPE, true>, grid, dim3(256), st, p)
+                     : launch_main(mt::attn_fwd_kernel<E, D, ROPE, false>, grid, dim3(256), st, p);
+  }
 }
 
 // stage: 1 = dQ (+ delta), 2 = dK/dV, 3 = both

@@ -73,6 +73,29 @@ def test_head_dims_and_dtypes(mta, d, dtype):
     compare(run_hip(mta, q, k, v, do, 4, cos, sin), oracle(q, k, v, do, 4, cos, sin))
 
 
+@pytest.mark.parametrize("pattern", ["ramp", "spike"])
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_online_softmax_rescales(mta, d, pattern):
+    """Running row max raised in the middle of tiles.
+
+    "ramp" grows the key magnitudes along the sequence, so the row max of
+    nearly every 32-key quarter exceeds the previous one by more than the
+    kernels' lazy-rescale slack; "spike" puts one dominant key in the third
+    quarter of the first tile and another in the second tile.  Both make the
+    forward rescale while the next quarter's scores are already in flight.
+    """
+    b, t, hq, hkv = 1, 300, 8, 2
+    q, k, v, do = make_inputs(b, t, hq, hkv, d, sigma=0.5, seed=7 + d)
+    if pattern == "ramp":
+        k = (k.float() * torch.linspace(1.0, 12.0, t).view(1, 1, t, 1)).to(k.dtype)
+    else:
+        k = k.float()
+        k[:, :, 70] *= 24.0
+        k[:, :, 190] *= 48.0
+        k = k.to(q.dtype)
+    compare(run_hip(mta, q, k, v, do, hq // hkv), oracle(q, k, v, do, hq // hkv))
+
+
 def test_reference_small_case_fp16(mta):
     """test_training.py:519-548: fp16, B=1, Hq=4, Hkv=2, T=17, D=32, seed 11,
     against the frozen SDPA output at the reference's own tolerance (5e-2/6e-2),
