@@ -16,12 +16,15 @@
 // in its epilogues (src/mega_trading/kernels/triton_ops.py:205-214).
 //
 // Tiling.  A "row block" is 64 query rows of one head.
-//   * forward / dQ: a workgroup is 4 waves; each wave owns one (query head,
-//     row block).  The 4 waves are the R_SUB = min(R, 4) heads of one KV group
-//     times 4/R_SUB consecutive row blocks, so every K/V tile staged in LDS
-//     feeds all of them (forward: 128-key tiles, dQ: 64-key tiles, both
-//     double-buffered).  S^T = K Q^T puts one query per lane (lane % 32),
-//     keys along the accumulator slots; the row max needs one lane^32 swap.
+//   * forward / dQ (D <= 64): a workgroup is 4 waves; each wave owns one
+//     (query head, row block).  The 4 waves are the R_SUB = min(R, 4) heads of
+//     one KV group times 4/R_SUB consecutive row blocks, so every K/V tile
+//     staged in LDS feeds all of them (forward: 128-key tiles, dQ: 64-key
+//     tiles, both double-buffered).  S^T = K Q^T puts one query per lane
+//     (lane % 32), keys along the accumulator slots; the row max needs one
+//     lane^32 swap.  At D = 128 the same (head, row block) pairs are split
+//     into two 32-row waves (8 waves per workgroup, two per SIMD), which keeps
+//     the wider rows within 256 registers.
 //   * dK/dV: a workgroup is 4 waves of 32 keys each (a 128-key block of one
 //     KV head, K and V held in registers); it walks (query head, 128-row step
 //     on or below the diagonal) with the Q / dO rows of each step staged in
@@ -321,7 +324,8 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
 // PEEL: as for the dQ kernel, the 4 waves share one row block, so the
 // diagonal (masked) tile is the last one and runs after the loop.
 template <class E, int D, bool ROPE, bool PEEL>
-__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
+  static_assert(D <= 64, "D = 128 uses attn_fwd_w8_kernel");
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;            // k-steps over d
@@ -678,9 +682,9 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
 // One 64-key K/V tile against the wave's 64 query rows: S^T and dP^T
 // recomputed (lane = query), P = 2^(S c2 - lse2), dS = P (dP - delta),
 // dQ += dS K.  With MASK (the diagonal tile) keys above the query get P = 0.
-// For D <= 64 the two 32-key halves mt run one after the other and each K / V
-// operand read from LDS (row reads for S^T / dP^T, transposed reads for dQ)
-// feeds both 32-query halves nt of the wave.
+// The two 32-key halves mt run one after the other and each K / V operand
+// read from LDS (row reads for S^T / dP^T, transposed reads for dQ) feeds
+// both 32-query halves nt of the wave.
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typename E::v8 (*qop)[D / 16],
                                         const typename E::v8 (*gop)[D / 16], f32x16 (*dqacc)[2], const float* lse2,
@@ -689,57 +693,6 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  if constexpr (D > 64) {
-    // D = 128: query halves outer (each re-reads the K / V operands), which
-    // keeps the one-wave-per-SIMD working set within the registers
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      f32x16 st[2], dpt[2];  // [mt]
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        {
-          const V8 a = TL::template row_op<E>(K, rbase, mt * 32, 0);
-          const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
-          st[mt] = E::mfma(a, qop[nt][0], f32x16{});
-          dpt[mt] = E::mfma(b, gop[nt][0], f32x16{});
-        }
-#pragma unroll
-        for (int kk = 1; kk < KT; ++kk) {
-          const V8 a = TL::template row_op<E>(K, rbase, mt * 32, kk);
-          const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, kk);
-          st[mt] = E::mfma(a, qop[nt][kk], st[mt]);
-          dpt[mt] = E::mfma(b, gop[nt][kk], dpt[mt]);
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        V8 dsb[2];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float pv = exp2_fast(__builtin_fmaf(st[mt][i], c2, -lse2[nt]));
-          if constexpr (MASK) {
-            const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-            if (kr > nt * 32 + l32) pv = 0.f;
-          }
-          st[mt][i] = pv * (dpt[mt][i] - dlt[nt]);
-        }
-        dsb[0] = pack8<E>(st[mt], 0);
-        dsb[1] = pack8<E>(st[mt], 8);
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const V8 a = TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt);
-            dqacc[dt][nt] = E::mfma(a, dsb[k2], dqacc[dt][nt]);
-          }
-        }
-      }
-      // keep the two halves' live ranges apart (the scheduler would
-      // otherwise interleave them and exceed the register budget)
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return;
-  }
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     f32x16 st[2], dpt[2];  // [nt]
@@ -796,7 +749,8 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
 // loop; keeping the masked tile out of the loop keeps the loop within the
 // register budget.
 template <class E, int D, bool ROPE, bool PEEL>
-__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
+  static_assert(D <= 64, "D = 128 uses attn_bwd_dq_w8_kernel");
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
@@ -924,6 +878,182 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void attn_bwd_dq_kernel(AttnP
   }
 }
 
+
+// ===========================================================================
+// Backward, dQ for D = 128: 8 waves of 32 query rows per workgroup
+// ===========================================================================
+// As for the D = 128 forward: the 4 (head, 64-row block) pairs of a RowTask
+// split into two 32-row waves, two waves per SIMD and no spills.  At D = 128
+// attn_bwd_dq_kernel re-reads the K / V operands for each 32-query half
+// anyway, so the narrower wave costs no extra LDS reads per MFMA.
+template <class E, int D, bool MASK>
+__device__ __forceinline__ void dq32_tile(const char* K, const char* Vr, const typename E::v8* qop,
+                                          const typename E::v8* gop, f32x16* dqacc, float lse2, float dlt, int rbase,
+                                          TrBase tbase, int l32, int hh, int qoff, float c2) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    // on the diagonal tile, key halves wholly above the wave's rows add nothing
+    if (MASK && mt * 32 > qoff + 31) continue;
+    f32x16 st, dpt;
+    {
+      const V8 a = TL::template row_op<E>(K, rbase, mt * 32, 0);
+      const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
+      st = E::mfma(a, qop[0], f32x16{});
+      dpt = E::mfma(b, gop[0], f32x16{});
+    }
+#pragma unroll
+    for (int kk = 1; kk < KT; ++kk) {
+      const V8 a = TL::template row_op<E>(K, rbase, mt * 32, kk);
+      const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, kk);
+      st = E::mfma(a, qop[kk], st);
+      dpt = E::mfma(b, gop[kk], dpt);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float pv = exp2_fast(__builtin_fmaf(st[i], c2, -lse2));
+      if constexpr (MASK) {
+        const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (kr > qoff + l32) pv = 0.f;
+      }
+      st[i] = pv * (dpt[i] - dlt);
+    }
+    V8 dsb[2];
+    dsb[0] = pack8<E>(st, 0);
+    dsb[1] = pack8<E>(st, 8);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        dqacc[dt] = E::mfma(TL::template tr_op<E>(K, tbase, 2 * mt + k2, dt), dsb[k2], dqacc[dt]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <class E, int D, bool ROPE, bool PEEL>
+__global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_bwd_dq_w8_kernel(AttnParams p) {
+  using V8 = typename E::v8;
+  using TL = Tile<D>;
+  constexpr int KT = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int SW = TL::INSTR < kFwdW8Waves ? TL::INSTR : kFwdW8Waves;  // waves that stage tiles
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
+
+  const RowTask task = row_task(p);
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int hh = lane >> 5;
+  const int pw = wave >> 1;
+  const int head = task.kvh * p.R + task.hs * p.r_sub + (pw % p.r_sub);
+  const int qb = task.sb * p.rb + pw / p.r_sub;
+  const int qoff = 32 * (wave & 1);                 // the wave's rows within its 64-row block
+  const int q0 = qb * kBlk + qoff;
+  const bool active = qb < p.nqb && q0 < p.T;
+  const int jlast = min(p.nqb - 1, task.sb * p.rb + p.rb - 1);
+
+  const uint16_t* kbase = p.k + task.b * p.sk[0] + (int64_t)task.kvh * p.sk[1];
+  const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
+  const int64_t rowbase = ((int64_t)task.b * p.Hq + head) * p.T;
+
+  V8 qop[KT], gop[KT];
+  float lse2, dlt;
+  {
+    const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
+    const uint16_t* gbase = p.dout + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
+    const uint16_t* obase = p.o + task.b * p.so[0] + (int64_t)head * p.so[1];
+    const int row = q0 + l32;
+    const int rc = min(row, p.T - 1);
+    const bool ok = active && row < p.T;
+    u32x4 qx[KT], gx[KT], ox[KT];
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      const int d0 = 16 * kk + 8 * hh;
+      qx[kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
+      gx[kk] = *reinterpret_cast<const u32x4*>(gbase + (int64_t)rc * p.sdo[2] + d0);
+      ox[kk] = *reinterpret_cast<const u32x4*>(obase + (int64_t)rc * p.so[2] + d0);
+    }
+    const float lx = p.lse[rowbase + rc];
+    float dsum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      qop[kk] = __builtin_bit_cast(V8, ok ? qx[kk] : zero4());
+      const u32x4 g = ok ? gx[kk] : zero4();
+      const u32x4 o = ox[kk];
+      gop[kk] = __builtin_bit_cast(V8, g);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) dsum += lo_f<E>(g[w]) * lo_f<E>(o[w]) + hi_f<E>(g[w]) * hi_f<E>(o[w]);
+    }
+    dsum = sum_with_partner(dsum);
+    dlt = dsum;
+    lse2 = ok ? lx * kLog2e : 0.f;
+    if (ok && hh == 0) {  // negated: the dK/dV pass seeds its accumulators with them
+      p.ndelta[rowbase + row] = -dsum;
+      p.nlse2[rowbase + row] = -lse2;
+    }
+  }
+
+  f32x16 dqacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) zero16(dqacc[dt]);
+
+  Stager<D, SW> ks_stage, vs_stage;
+  const bool stager = wave < SW;
+  ks_stage.init(p.sk[2], wave, lane);
+  vs_stage.init(p.sv[2], wave, lane);
+  const int rbase_op = TL::row_base(lane);
+  const TrBase tbase_op = TL::tr_base(lane);
+
+  if (stager) {
+    ks_stage.stage(smem[0][0], kbase, p.sk[2], 0, p.T);
+    vs_stage.stage(smem[0][1], vbase, p.sv[2], 0, p.T);
+  }
+  wait_vmem();
+  __syncthreads();
+
+  const float c2 = p.scale_log2;
+  for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
+    const int buf = j & 1;
+    if (j < jlast && stager) {
+      ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
+      vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
+    }
+    if (active && j <= qb) {
+      if (PEEL || j < qb)
+        dq32_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh,
+                               qoff, c2);
+      else
+        dq32_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh,
+                              qoff, c2);
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+  if (PEEL && active)  // qb == jlast
+    dq32_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op,
+                          l32, hh, qoff, c2);
+
+  if (!active) return;
+  const int row = q0 + l32;
+  if (row >= p.T) return;
+  uint16_t* dqbase = p.out + task.b * p.sout[0] + (int64_t)head * p.sout[1];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = dt * 32 + 8 * g + 4 * hh;
+      float x0 = dqacc[dt][4 * g] * p.scale, x1 = dqacc[dt][4 * g + 1] * p.scale;
+      float x2 = dqacc[dt][4 * g + 2] * p.scale, x3 = dqacc[dt][4 * g + 3] * p.scale;
+      if constexpr (ROPE)
+        rope_back4(x0, x1, x2, x3, p.cos + (int64_t)row * (D / 2) + d / 2, p.sin + (int64_t)row * (D / 2) + d / 2);
+      u32x2 w = {pack2<E>(x0, x1), pack2<E>(x2, x3)};
+      *reinterpret_cast<u32x2*>(dqbase + (int64_t)row * p.sout[2] + d) = w;
+    }
+}
 
 // dK/dV softmax step for one 32-row quarter (C layout: lane = key, slots =
 // rows).  The score MFMAs start from the accumulator tiles -lse2[row] and

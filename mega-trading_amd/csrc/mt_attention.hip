@@ -177,8 +177,15 @@ template <class E, int D, bool ROPE>
 hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
   if (stage & 1) {
     dim3 grid_dq(p.nsb * p.B * p.Hkv * p.n_hsub);
-    hipError_t e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE, true>, grid_dq, dim3(256), st, p)
-                             : launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE, false>, grid_dq, dim3(256), st, p);
+    hipError_t e;
+    if constexpr (D > 64) {
+      const dim3 block(64 * mt::kFwdW8Waves);
+      e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, true>, grid_dq, block, st, p)
+                    : launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, false>, grid_dq, block, st, p);
+    } else {
+      e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE, true>, grid_dq, dim3(256), st, p)
+                    : launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE, false>, grid_dq, dim3(256), st, p);
+    }
     if (e != hipSuccess) return e;
   }
   if (stage & 2) {
