@@ -15,7 +15,8 @@
 * cpu_baseline: the reference's CPU attention path (torch SDPA, fp32, forward
   + autograd backward, model.py:228-235) on the host cores over a bounded
   sample of the same workload.
-* secondary: BASELINE config 2 (T=1024) fwd+bwd TFLOP/s, the un-fused op, and
+* secondary: BASELINE config 2 (T=1024) and config 4 (D=128) fwd+bwd TFLOP/s,
+  the un-fused op, and
   train tokens/sec of the 8-layer decoder with the HIP
   attention in every layer against the same model on the reference's SDPA
   route (the "train tokens/sec" half of the metric).
@@ -52,6 +53,7 @@ METRIC = "causal GQA fwd+bwd TFLOP/s (% bf16 MFMA peak) at T=1k/4k; train tokens
 # (B, T, Hq, Hkv, D)
 C2 = (16, 1024, 8, 2, 64)
 C3 = (4, 4096, 16, 4, 64)
+C4 = (8, 2048, 32, 8, 128)
 
 # algorithmic MFMA FLOPs per launch, in units of B * Hq * D * T(T+1)/2
 KERNEL_FLOP_UNITS = {
@@ -468,6 +470,7 @@ def main(argv=None) -> int:
 
     ms_c2, _ = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)
     ms_c3_plain, _ = time_op_steps(pkg, C3, max(10, args.steps // 2), 3, rope=False)
+    ms_c4, _ = time_op_steps(pkg, C4, max(10, args.steps // 4), 3, rope=True)
     ceiling = mfma_ceiling()
     ops_line = time_ops(pkg)
 
@@ -506,6 +509,8 @@ def main(argv=None) -> int:
             "C2_fwd_bwd_tflops": round(fwd_bwd_flops(*C2[:1], C2[1], C2[2], C2[4]) / (ms_c2 * 1e-3) / 1e12, 2),
             "C2_ms_per_step": round(ms_c2, 4),
             "C3_unfused_rope_free_tflops": round(flops / (ms_c3_plain * 1e-3) / 1e12, 2),
+            "C4_fwd_bwd_tflops": round(fwd_bwd_flops(C4[0], C4[1], C4[2], C4[4]) / (ms_c4 * 1e-3) / 1e12, 2),
+            "C4_ms_per_step": round(ms_c4, 4),
             "wall_ms_per_step": round(ms_wall, 4),
         },
     }
