@@ -116,6 +116,25 @@ __device__ __forceinline__ void lds_dma4(const float* g, char* l) {
   asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
 }
 
+// Scalar-base forms: lane L reads base + voff_L (a 32-bit byte offset), so a
+// whole tile's addresses cost one 64-bit scalar add and no vector ALU work.
+// `base` must be wave-uniform; it is moved to scalar registers explicitly
+// (free when the compiler already holds it there).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t voff, uint32_t l) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(l));
+}
+
+__device__ __forceinline__ void lds_dma4_s(const void* base, uint32_t voff, uint32_t l) {
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(l));
+}
+
 // Staging of one 64-row tile by the NW waves of a workgroup: per-lane source
 // offsets (elements, relative to the tile's first row) of the INSTR/NW wave
 // instructions this wave issues, computed once.
@@ -125,8 +144,8 @@ struct Stager {
   using TL = Tile<D>;
   static_assert(TL::INSTR % NW == 0, "tile instructions must split evenly over the waves");
   static constexpr int N = TL::INSTR / NW;
-  int off[N];   // row * row_stride + chunk * 8
-  int lds_off;  // byte offset of this wave's first 1 KB block in the tile
+  uint32_t voff[N];  // byte offsets (row * row_stride + chunk * 8) * 2 from the tile's first row
+  int lds_off;       // byte offset of this wave's first 1 KB block in the tile (wave-uniform)
   int wave_, lane_;
 
   static __device__ __forceinline__ void place(int i, int wave, int lane, int& row, int& chunk) {
@@ -140,9 +159,9 @@ struct Stager {
     for (int i = 0; i < N; ++i) {
       int row, chunk;
       place(i, wave, lane, row, chunk);
-      off[i] = row * (int)row_stride + chunk * 8;
+      voff[i] = (uint32_t)(row * (int)row_stride + chunk * 8) * 2u;
     }
-    lds_off = wave * 1024;
+    lds_off = __builtin_amdgcn_readfirstlane(wave) * 1024;
     wave_ = wave;
     lane_ = lane;
   }
@@ -151,8 +170,9 @@ struct Stager {
   __device__ __forceinline__ void stage(char* lds, const uint16_t* src, int64_t row_stride, int row0, int T) const {
     if (row0 + 64 <= T) {
       const uint16_t* tile = src + (int64_t)row0 * row_stride;
+      const uint32_t l0 = lds_addr(lds) + (uint32_t)lds_off;
 #pragma unroll
-      for (int i = 0; i < N; ++i) lds_dma16(tile + off[i], lds + lds_off + i * NW * 1024);
+      for (int i = 0; i < N; ++i) lds_dma16_s(tile, voff[i], l0 + i * NW * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < N; ++i) {
@@ -167,7 +187,10 @@ struct Stager {
 
 // Stage 64 fp32 values (row-indexed vector, clamped at T-1) with one wave.
 __device__ __forceinline__ void stage_vec64(char* lds, const float* src, int row0, int T, int lane) {
-  lds_dma4(src + min(row0 + lane, T - 1), lds);
+  if (row0 + 64 <= T)
+    lds_dma4_s(src + row0, (uint32_t)lane * 4u, lds_addr(lds));
+  else
+    lds_dma4(src + min(row0 + lane, T - 1), lds);
 }
 
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
