@@ -63,6 +63,20 @@ def test_ragged_lengths_and_group_sizes(mta, t, hq, hkv):
     compare(run_hip(mta, q, k, v, do, r, cos, sin), oracle(q, k, v, do, r, cos, sin))
 
 
+@pytest.mark.parametrize("t", [1, 31, 33, 65, 127, 129, 200])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (6, 2), (8, 2)])
+@pytest.mark.parametrize("d", [32, 128])
+def test_ragged_lengths_other_head_dims(mta, d, t, hq, hkv):
+    """Ragged T and every workgroup shape (R = 1, 3, 4) at D = 32 and D = 128;
+    at D = 128 the forward and dQ split each 64-row block into two 32-row
+    waves, so T just below / above a 32- or 64-row boundary matters."""
+    r = hq // hkv
+    q, k, v, do = make_inputs(2, t, hq, hkv, d, sigma=0.5, seed=t * 10 + hq + d)
+    cos, sin = orc.rope_tables(t, d, 10_000.0)
+    compare(run_hip(mta, q, k, v, do, r), oracle(q, k, v, do, r))
+    compare(run_hip(mta, q, k, v, do, r, cos, sin), oracle(q, k, v, do, r, cos, sin))
+
+
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 def test_head_dims_and_dtypes(mta, d, dtype):
