@@ -42,6 +42,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
   __shared__ float qs[kDecMaxR][D];
   __shared__ float ps[kDecMaxR][kDecSplit];
   __shared__ float red[kDecMaxR][4];
+  __shared__ float red_buf[(256 / (D / 8)) * kDecMaxR * D];  // V-pass key-group sums (64 KB)
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -112,25 +113,53 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
   }
   __syncthreads();
 
-  // o[h][d] = sum_j p[h][j] V[k0 + j][d]: a wave reads V rows coalesced along d
+  // o[h][d] = sum_j p[h][j] V[k0 + j][d].  Thread t takes the 8-value d chunk
+  // c = t % NC of keys j = t / NC, t / NC + G, ... (one 16-byte load per key
+  // feeds 8 d values of every head), then the G key groups are summed
+  // through LDS.
+  constexpr int NC = D / 8;      // 16-byte chunks per V row
+  constexpr int G = 256 / NC;    // key groups
   const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2];
+  const int c = tid % NC;
+  float acc[kDecMaxR][8];
+#pragma unroll
+  for (int h = 0; h < kDecMaxR; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+#pragma unroll 4
+  for (int j = tid / NC; j < n; j += G) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(vbase + (int64_t)j * p.sv[2] + 8 * c);
+    float vv[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vv[2 * e] = lo_f<E>(w[e]);
+      vv[2 * e + 1] = hi_f<E>(w[e]);
+    }
+#pragma unroll
+    for (int h = 0; h < kDecMaxR; ++h) {
+      if (h < R) {
+        const float pj = ps[h][j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(pj, vv[e], acc[h][e]);
+      }
+    }
+  }
+  // key-group partial sums: red_o[g][h][d]
+  float* red_o = red_buf;
+  const int kg = tid / NC;
+#pragma unroll
+  for (int h = 0; h < kDecMaxR; ++h)
+    if (h < R)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red_o[(kg * kDecMaxR + h) * D + 8 * c + e] = acc[h][e];
+  __syncthreads();
   for (int i = tid; i < R * D; i += 256) {
     const int h = i / D, d = i % D;
-    float acc = 0.f;
-    int j = 0;
-    for (; j + 4 <= n; j += 4) {
-      const float v0 = E::to_f(vbase[(int64_t)(j + 0) * p.sv[2] + d]);
-      const float v1 = E::to_f(vbase[(int64_t)(j + 1) * p.sv[2] + d]);
-      const float v2 = E::to_f(vbase[(int64_t)(j + 2) * p.sv[2] + d]);
-      const float v3 = E::to_f(vbase[(int64_t)(j + 3) * p.sv[2] + d]);
-      acc = __builtin_fmaf(ps[h][j], v0, acc);
-      acc = __builtin_fmaf(ps[h][j + 1], v1, acc);
-      acc = __builtin_fmaf(ps[h][j + 2], v2, acc);
-      acc = __builtin_fmaf(ps[h][j + 3], v3, acc);
-    }
-    for (; j < n; ++j) acc = __builtin_fmaf(ps[h][j], E::to_f(vbase[(int64_t)j * p.sv[2] + d]), acc);
+    float o = 0.f;
+#pragma unroll 8
+    for (int gg = 0; gg < G; ++gg) o += red_o[(gg * kDecMaxR + h) * D + d];
     float* dst = p.part + (((int64_t)b * p.Hq + kvh * R + h) * p.nsplit + s) * (D + 2);
-    dst[d] = acc;
+    dst[d] = o;
     if (d == 0) {
       dst[D] = m[h];
       dst[D + 1] = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
