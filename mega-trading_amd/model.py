@@ -106,6 +106,9 @@ class TradingModel(nn.Module):
 
     # KV-cached generate on the HIP routes replays one recorded HIP graph per token
     decode_graphs = True
+    # (batch, device, per-layer KV caches, recorded decode step) kept between
+    # generate calls so later calls with the same batch reuse the recording
+    _gen_state = None
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         return self.output(self._hidden(input_ids))
@@ -150,16 +153,24 @@ class TradingModel(nn.Module):
             return self._generate_recompute(input_ids, max_new_tokens, top_k)
         tokens = input_ids
         cache = step = None
+        key = (tokens.shape[0], tokens.device)
         for _ in range(max_new_tokens):
             t = tokens.shape[1]
             if t > self.block_size:
                 cache = step = None
                 logits = self(tokens[:, -self.block_size:])[:, -1, :]
             elif cache is None:
-                logits, cache = self._prefill(tokens)
+                # prefill into the kept caches when a recording for this batch exists
+                state = self._gen_state if self.decode_graphs else None
+                reuse = state is not None and state[0] == key
+                logits, cache, reused = self._prefill(tokens, state[1] if reuse else None)
+                step = state[2] if reuse and reused else None
+                if reuse and not reused:
+                    self._gen_state = None
             elif self.decode_graphs:
                 if step is None:
                     step = _DecodeGraph(self, cache, tokens.shape[0], tokens.device)
+                    self._gen_state = (key, cache, step)
                 logits = step(tokens[:, -1:], t - 1)
             else:
                 logits = self._decode(tokens[:, -1:], cache, t - 1)
@@ -176,16 +187,21 @@ class TradingModel(nn.Module):
             tokens = torch.cat([tokens, _sample_next(logits, top_k)], dim=1)
         return tokens
 
-    def _prefill(self, tokens: torch.Tensor):
-        """Forward over the prompt that also returns per-layer KV caches of capacity block_size."""
+    def _prefill(self, tokens: torch.Tensor, into=None):
+        """Forward over the prompt that also fills per-layer KV caches of capacity
+        block_size: the caches given in ``into`` when their shape and dtype fit
+        (then ``reused`` is True), else new ones.  Returns (logits, caches, reused)."""
         hidden = self.token_embedding(tokens)
         cache = []
-        for block in self.blocks:
-            attended, k_cache, v_cache = block.attention.prefill(block.attention_norm(hidden), self.block_size)
+        reused = into is not None
+        for i, block in enumerate(self.blocks):
+            attended, k_cache, v_cache = block.attention.prefill(
+                block.attention_norm(hidden), self.block_size, into[i] if into is not None else None)
+            reused = reused and k_cache is into[i][0]
             cache.append((k_cache, v_cache))
             hidden = hidden + attended
             hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
-        return self.output(self.norm(hidden))[:, -1, :], cache
+        return self.output(self.norm(hidden))[:, -1, :], cache, reused
 
     def _decode(self, token: torch.Tensor, cache, pos) -> torch.Tensor:
         """Logits after the token at position ``pos`` (its K/V are appended to the
@@ -306,9 +322,11 @@ class LlamaAttention(nn.Module):
         value = self.v_proj(hidden).view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
         return query, key, value
 
-    def prefill(self, hidden: torch.Tensor, capacity: int):
+    def prefill(self, hidden: torch.Tensor, capacity: int, into=None):
         """Attention over the prompt (fused-RoPE HIP kernels) plus KV caches
-        [B, Hkv, capacity, D] holding its rotated keys and values (16-bit)."""
+        [B, Hkv, capacity, D] holding its rotated keys and values (16-bit);
+        ``into`` = (k_cache, v_cache) to fill instead of allocating, used when
+        its shape and dtype match."""
         b, t, hidden_dim = hidden.shape
         query, key, value = self._heads(hidden)
         kdt = query.dtype if query.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
@@ -316,8 +334,12 @@ class LlamaAttention(nn.Module):
         cos, sin = _rope_tables(self.rope.cos, self.rope.sin, q16)
         out, _lse, _q_rot, k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(
             q16, k16, v16, cos, sin, 1.0 / math.sqrt(self.head_dim))
-        k_cache = torch.empty((b, self.kv_heads, capacity, self.head_dim), device=hidden.device, dtype=kdt)
-        v_cache = torch.empty_like(k_cache)
+        shape = (b, self.kv_heads, capacity, self.head_dim)
+        if into is not None and into[0].shape == shape and into[0].dtype == kdt and into[0].device == hidden.device:
+            k_cache, v_cache = into
+        else:
+            k_cache = torch.empty(shape, device=hidden.device, dtype=kdt)
+            v_cache = torch.empty_like(k_cache)
         k_cache[:, :, :t] = k_rot
         v_cache[:, :, :t] = v16
         attended = out.to(hidden.dtype).transpose(1, 2).contiguous().view(b, t, hidden_dim)

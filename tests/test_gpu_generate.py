@@ -88,7 +88,7 @@ def test_cached_logits_match_full_recompute(backend):
     g = torch.Generator().manual_seed(11)
     tokens = torch.randint(0, 128, (3, 40), generator=g).cuda()
     with torch.no_grad():
-        logits, cache = m._prefill(tokens[:, :10])
+        logits, cache, _ = m._prefill(tokens[:, :10])
         assert _rel(logits, m(tokens[:, :10])[:, -1, :]) < 2e-2
         for pos in range(10, 40):  # teacher forcing: feed the true next token
             step = m._decode(tokens[:, pos:pos + 1], cache, pos)
@@ -152,7 +152,7 @@ def test_graph_decode_replays_match_eager_decode():
     g = torch.Generator().manual_seed(31)
     tokens = torch.randint(0, 128, (4, 30), generator=g).cuda()
     with torch.no_grad():
-        _, cache_a = m._prefill(tokens[:, :12])
+        _, cache_a, _ = m._prefill(tokens[:, :12])
         cache_b = [(k.clone(), v.clone()) for k, v in cache_a]
         step = model_mod._DecodeGraph(m, cache_b, 4, tokens.device)
         for pos in range(12, 30):
@@ -174,3 +174,26 @@ def test_generate_with_graphs_equals_without():
     m.decode_graphs = True
     b = m.generate(prompt, max_new_tokens=45, top_k=1)
     assert torch.equal(a, b)
+
+
+def test_generate_reuses_the_recorded_step_across_calls():
+    # a second generate call with the same batch prefills into the kept caches
+    # and replays the same recording; its tokens equal a fresh model's and the
+    # eager (graph-free) path's; another batch size records anew
+    m = _model("hip", block_size=48)
+    g = torch.Generator().manual_seed(33)
+    p1 = torch.randint(0, 128, (3, 10), generator=g).cuda()
+    p2 = torch.randint(0, 128, (3, 14), generator=g).cuda()
+    first = m.generate(p1, max_new_tokens=20, top_k=1)
+    state = m._gen_state
+    assert state is not None and state[0][0] == 3
+    second = m.generate(p2, max_new_tokens=20, top_k=1)
+    assert m._gen_state is state  # same caches and recording
+    fresh = _model("hip", block_size=48)
+    fresh.decode_graphs = False
+    assert torch.equal(first, fresh.generate(p1, max_new_tokens=20, top_k=1))
+    assert torch.equal(second, fresh.generate(p2, max_new_tokens=20, top_k=1))
+    p3 = torch.randint(0, 128, (5, 9), generator=g).cuda()
+    third = m.generate(p3, max_new_tokens=8, top_k=1)
+    assert m._gen_state is not state and m._gen_state[0][0] == 5
+    assert torch.equal(third, fresh.generate(p3, max_new_tokens=8, top_k=1))
