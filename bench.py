@@ -363,7 +363,8 @@ def train_tokens_per_second(pkg, steps, warmup):
     """the 8-layer decoder train step on the same seeded
     weights and Zipf batch through three routes:
       hip    -- every HIP operator of this package (attention with fused RoPE,
-                SwiGLU gate, RMSNorm);
+                packed SwiGLU gate, RMSNorm) and its projections (q/k/v and
+                w1/w3 each one GEMM, split-K fp32 weight gradients);
       triton -- the reference's own Triton routing with the HIP kernels in its
                 place (attention + SwiGLU gate; norms stay torch, model.py:166,176);
       sdpa   -- the reference's eager route (SDPA + torch ops): the baseline.

@@ -18,6 +18,9 @@
  *                           reached from triton_swiglu_gate :57-61 and
  *                           SwiGLU.forward, src/mega_trading/model.py:252-253
  *   mt_swiglu_bwd        <- _TritonSwiGLUGate.backward :455-474 (kernel :799-819)
+ *   mt_swiglu_packed_fwd / _bwd  no counterpart: the same gate on the packed
+ *                           output of one GEMM against the stacked (w1; w3)
+ *                           weights (this build's "hip" decoder route)
  *   mt_cross_entropy_rows <- _fused_ce_row_kernel :822-887, the per-chunk loss and
  *                           in-place logits-gradient step of
  *                           _TritonFusedLinearCrossEntropy.forward :312-400,
@@ -83,6 +86,18 @@ int mt_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dt
 /* dgate = round(dout * up) * sig * (1 + gate (1 - sig)), dup = dout * round(silu(gate)). */
 int mt_swiglu_bwd(const void* gate, const void* up, const void* dout, void* dgate, void* dup, int64_t n, int dtype,
                   void* stream);
+
+/* The same gate on the packed [rows, 2*cols] output of one GEMM against the
+ * stacked (w1; w3) weights: gate = columns [0, cols) and up = [cols, 2*cols) of
+ * each row; out [rows, cols] contiguous.  No counterpart in the reference (its
+ * gate takes the two products separately, triton_ops.py:57-61): the packed form
+ * lets the two FFN input projections share one GEMM without copies.
+ * cols % 8 == 0, rows * cols / 8 < 2^31, pointers 16-byte aligned. */
+int mt_swiglu_packed_fwd(const void* gu, void* out, int64_t rows, int64_t cols, int dtype, void* stream);
+
+/* Backward of mt_swiglu_packed_fwd: dgu (gu's packed layout) = (dgate | dup) as in mt_swiglu_bwd. */
+int mt_swiglu_packed_bwd(const void* gu, const void* dout, void* dgu, int64_t rows, int64_t cols, int dtype,
+                         void* stream);
 
 /* Cross-entropy rows: for each of `rows` rows of `vocab` logits (row stride
  * row_stride elements, dtype), loss_rows[r] = (logsumexp(row) - row[labels[r]]) / n_valid,

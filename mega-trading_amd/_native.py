@@ -35,6 +35,8 @@ EXPORTS = (
     "mt_add_rms_norm_bwd",
     "mt_swiglu_fwd",
     "mt_swiglu_bwd",
+    "mt_swiglu_packed_fwd",
+    "mt_swiglu_packed_bwd",
     "mt_cross_entropy_rows",
     "mt_gqa_attn_decode_workspace_size",
     "mt_gqa_attn_decode",
@@ -60,6 +62,8 @@ _OPS_SIGNATURES = {
     "mt_add_rms_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
     "mt_swiglu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "mt_swiglu_bwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _P]),
+    "mt_swiglu_packed_fwd": (_I, [_P, _P, _L, _L, _I, _P]),
+    "mt_swiglu_packed_bwd": (_I, [_P, _P, _P, _L, _L, _I, _P]),
     "mt_cross_entropy_rows": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _I, _I, _P]),
     "mt_gqa_attn_decode_workspace_size": (_S, [_I, _I, _I, _I]),
     "mt_gqa_attn_decode": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _S, _P]),

@@ -275,6 +275,51 @@ int mt_swiglu_bwd(const void* gate, const void* up, const void* dout, void* dgat
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }
 
+namespace {
+int check_packed(int64_t rows, int64_t cols) {
+  if (rows < 0 || cols < 0 || cols % 8)
+    return fail(MT_E_SHAPE, "rows %lld and cols %lld must be >= 0 with cols a multiple of 8", (long long)rows,
+                (long long)cols);
+  if (rows * (cols / 8) >= (int64_t(1) << 31))
+    return fail(MT_E_SHAPE, "rows * cols / 8 must be below 2^31 (got %lld)", (long long)(rows * (cols / 8)));
+  return MT_OK;
+}
+}  // namespace
+
+int mt_swiglu_packed_fwd(const void* gu, void* out, int64_t rows, int64_t cols, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, dtype)) || (rc = check_packed(rows, cols))) return rc;
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_ptr("gu", gu)) || (rc = check_ptr("out", out))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int r = (int)rows, cpr = (int)(cols / 8);
+  const dim3 grid(swiglu_blocks(rows * cols));
+  if (dtype == MT_DTYPE_BF16) hipLaunchKernelGGL((K::swiglu_packed_fwd_kernel<K::kDtBF16>), grid, dim3(256), 0, st, gu, out, r, cpr);
+  else if (dtype == MT_DTYPE_FP16) hipLaunchKernelGGL((K::swiglu_packed_fwd_kernel<K::kDtFP16>), grid, dim3(256), 0, st, gu, out, r, cpr);
+  else hipLaunchKernelGGL((K::swiglu_packed_fwd_kernel<K::kDtFP32>), grid, dim3(256), 0, st, gu, out, r, cpr);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_swiglu_packed_bwd(const void* gu, const void* dout, void* dgu, int64_t rows, int64_t cols, int dtype,
+                         void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, dtype)) || (rc = check_packed(rows, cols))) return rc;
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_ptr("gu", gu)) || (rc = check_ptr("dout", dout)) || (rc = check_ptr("dgu", dgu))) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int r = (int)rows, cpr = (int)(cols / 8);
+  const dim3 grid(swiglu_blocks(rows * cols));
+  if (dtype == MT_DTYPE_BF16)
+    hipLaunchKernelGGL((K::swiglu_packed_bwd_kernel<K::kDtBF16>), grid, dim3(256), 0, st, gu, dout, dgu, r, cpr);
+  else if (dtype == MT_DTYPE_FP16)
+    hipLaunchKernelGGL((K::swiglu_packed_bwd_kernel<K::kDtFP16>), grid, dim3(256), 0, st, gu, dout, dgu, r, cpr);
+  else
+    hipLaunchKernelGGL((K::swiglu_packed_bwd_kernel<K::kDtFP32>), grid, dim3(256), 0, st, gu, dout, dgu, r, cpr);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
 int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* labels, int64_t rows, int vocab,
                           const int64_t* n_valid, int64_t ignore_index, float* loss_rows, int write_grad, int dtype,
                           void* stream) {

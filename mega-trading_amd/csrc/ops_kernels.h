@@ -372,6 +372,50 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const
   }
 }
 
+// The same gate over the packed output of one GEMM against the stacked
+// (w1; w3) weights: row r of `gu` holds gate in columns [0, cols) and up in
+// [cols, 2 cols); `out` is [rows, cols] and the backward's `dgu` has gu's
+// layout.  cols % 8 == 0; thread i takes the 8-value chunk (r, c) =
+// (i / cpr, i % cpr), cpr = cols / 8, with rows * cpr < 2^31.
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_packed_fwd_kernel(const void* gu, void* out, int rows, int cpr) {
+  const int n = rows * cpr;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    const int r = i / cpr, c = i - r * cpr;
+    const int64_t g0 = (int64_t)r * (16 * cpr) + 8 * c;
+    float g[8], u[8], o[8];
+    IO<DT>::load8(gu, g0, g);
+    IO<DT>::load8(gu, g0 + 8 * cpr, u);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[j] / (1.f + expf(-g[j]))) * u[j];
+    IO<DT>::store8(out, 8 * (int64_t)i, o);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_packed_bwd_kernel(const void* gu, const void* dout, void* dgu, int rows,
+                                                                int cpr) {
+  const int n = rows * cpr;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    const int r = i / cpr, c = i - r * cpr;
+    const int64_t g0 = (int64_t)r * (16 * cpr) + 8 * c;
+    float g[8], u[8], dy[8], dg[8], du[8];
+    IO<DT>::load8(gu, g0, g);
+    IO<DT>::load8(gu, g0 + 8 * cpr, u);
+    IO<DT>::load8(dout, 8 * (int64_t)i, dy);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = expf(-g[j]);
+      const float sg = 1.f / (1.f + e);
+      const float t = IO<DT>::round(dy[j] * u[j]);
+      dg[j] = (t * sg) * (1.f + g[j] * (1.f - sg));
+      du[j] = dy[j] * IO<DT>::round(g[j] / (1.f + e));
+    }
+    IO<DT>::store8(dgu, g0, dg);
+    IO<DT>::store8(dgu, g0 + 8 * cpr, du);
+  }
+}
+
 // ===========================================================================
 // Cross-entropy over rows of logits (the loss head of the fused linear
 // cross-entropy).  One workgroup (256 threads) per row of V logits:

@@ -43,6 +43,9 @@ from .attention import rope_attention as _hip_rope_attention
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
 from .ops import rms_norm as _hip_rms_norm
 from .ops import swiglu_gate as _hip_swiglu_gate
+from .ops import swiglu_gate_packed as _hip_swiglu_gate_packed
+from .projection import project as _project
+from .projection import project_packed as _project_packed
 
 __all__ = ["TradingModel", "LlamaDecoderBlock", "LlamaAttention", "SwiGLU", "RMSNorm", "RotaryEmbedding",
            "ATTENTION_BACKENDS", "HIP_BACKENDS"]
@@ -296,10 +299,7 @@ class LlamaAttention(nn.Module):
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         batch_size, sequence_length, hidden_dim = hidden.shape
-        # [B, T, H*D] -> [B, H, T, D] strided views, as model.py:220-222
-        query = self.q_proj(hidden).view(batch_size, sequence_length, self.attention_heads, self.head_dim).transpose(1, 2)
-        key = self.k_proj(hidden).view(batch_size, sequence_length, self.kv_heads, self.head_dim).transpose(1, 2)
-        value = self.v_proj(hidden).view(batch_size, sequence_length, self.kv_heads, self.head_dim).transpose(1, 2)
+        query, key, value = self._heads(hidden)
         dropout_p = self.dropout if self.training else 0.0
         if self.attention_backend in HIP_BACKENDS and dropout_p == 0.0:
             if self.fuse_rope:
@@ -313,14 +313,25 @@ class LlamaAttention(nn.Module):
                 query, key, value, dropout_p=dropout_p, is_causal=True, enable_gqa=self.repeats > 1
             )
         attended = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, hidden_dim)
-        return self.o_proj(attended)
+        return self._out(attended)
 
     def _heads(self, hidden: torch.Tensor):
+        """[B, T, H*D] projections -> [B, H, T, D] strided views, as model.py:220-222.
+        On "hip" the three products come from one GEMM (``projection.project``)."""
         b, t, _ = hidden.shape
-        query = self.q_proj(hidden).view(b, t, self.attention_heads, self.head_dim).transpose(1, 2)
-        key = self.k_proj(hidden).view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
-        value = self.v_proj(hidden).view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
+        if self.attention_backend == "hip":
+            query, key, value = _project(hidden, (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+        else:
+            query, key, value = self.q_proj(hidden), self.k_proj(hidden), self.v_proj(hidden)
+        query = query.view(b, t, self.attention_heads, self.head_dim).transpose(1, 2)
+        key = key.view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
+        value = value.view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
         return query, key, value
+
+    def _out(self, attended: torch.Tensor) -> torch.Tensor:
+        if self.attention_backend == "hip":
+            return _project_packed(attended, (self.o_proj.weight,))
+        return self.o_proj(attended)
 
     def prefill(self, hidden: torch.Tensor, capacity: int, into=None):
         """Attention over the prompt (fused-RoPE HIP kernels) plus KV caches
@@ -343,7 +354,7 @@ class LlamaAttention(nn.Module):
         k_cache[:, :, :t] = k_rot
         v_cache[:, :, :t] = v16
         attended = out.to(hidden.dtype).transpose(1, 2).contiguous().view(b, t, hidden_dim)
-        return self.o_proj(attended), k_cache, v_cache
+        return self._out(attended), k_cache, v_cache
 
     def decode(self, hidden: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos, length=None):
         """One token at position ``pos`` (int or device int32 tensor): rotate its
@@ -355,7 +366,7 @@ class LlamaAttention(nn.Module):
         out = _hip_decode_attention(q_rot, k_cache, v_cache, pos + 1 if length is None else length,
                                     repeats=self.repeats)
         attended = out.to(hidden.dtype).transpose(1, 2).reshape(b, 1, hidden_dim)
-        return self.o_proj(attended)
+        return self._out(attended)
 
 
 class SwiGLU(nn.Module):
@@ -370,6 +381,10 @@ class SwiGLU(nn.Module):
         self.operator_backend = operator_backend
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        if self.operator_backend == "hip":
+            # one GEMM for w1 and w3, the gate on its packed output, split-K dW
+            gated = _hip_swiglu_gate_packed(_project_packed(hidden, (self.w1.weight, self.w3.weight)))
+            return _project_packed(self.dropout(gated), (self.w2.weight,))
         gate = self.w1(hidden)
         up = self.w3(hidden)
         if self.operator_backend in HIP_BACKENDS:

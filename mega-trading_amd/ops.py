@@ -25,7 +25,8 @@ import torch
 
 from . import _native
 
-__all__ = ["rms_norm", "add_rms_norm", "swiglu_gate", "fused_linear_cross_entropy", "MAX_NORM_DIM"]
+__all__ = ["rms_norm", "add_rms_norm", "swiglu_gate", "swiglu_gate_packed", "fused_linear_cross_entropy",
+           "MAX_NORM_DIM"]
 
 MAX_NORM_DIM = 4096
 _DT = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16, torch.float32: _native.DTYPE_FP32}
@@ -63,6 +64,18 @@ def swiglu_gate(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     if up.dtype != gate.dtype or up.device != gate.device:
         raise RuntimeError("up must have the dtype and device of gate")
     return torch.ops.mega_trading_amd.swiglu_fwd(gate, up)
+
+
+def swiglu_gate_packed(gate_up: torch.Tensor) -> torch.Tensor:
+    """``swiglu_gate(gate, up)`` on the packed [..., 2F] output of one GEMM
+    against the stacked (w1; w3) weights: gate = the first F columns of each
+    row, up = the last F.  Returns [..., F].  No reference counterpart (the
+    reference gate takes the two products, ``triton_ops.py:57-61``); the
+    arithmetic and roundings are ``swiglu_gate``'s."""
+    _check_device_dtype(gate_up, "gate_up")
+    if gate_up.ndim < 1 or gate_up.shape[-1] % 16:
+        raise ValueError("gate_up's last dim must be 2F with F a multiple of 8")
+    return torch.ops.mega_trading_amd.swiglu_packed_fwd(gate_up)
 
 
 def fused_linear_cross_entropy(
@@ -292,6 +305,43 @@ def _swiglu_bwd_fake(gate, up, dout):
             torch.empty_like(gate, memory_format=torch.contiguous_format))
 
 
+@torch.library.custom_op("mega_trading_amd::swiglu_packed_fwd", mutates_args=(), device_types="cuda")
+def swiglu_packed_fwd(gate_up: torch.Tensor) -> torch.Tensor:
+    lib = _native.load()
+    gu = _flat(gate_up)
+    cols = gu.shape[-1] // 2
+    rows = gu.numel() // max(2 * cols, 1)
+    out = torch.empty((*gu.shape[:-1], cols), device=gu.device, dtype=gu.dtype)
+    with torch.cuda.device(gu.device):
+        rc = lib.mt_swiglu_packed_fwd(gu.data_ptr(), out.data_ptr(), rows, cols, _DT[gu.dtype], _stream(gu))
+    _native.check(rc, "mt_swiglu_packed_fwd")
+    return out
+
+
+@swiglu_packed_fwd.register_fake
+def _swiglu_packed_fwd_fake(gate_up):
+    return gate_up.new_empty((*gate_up.shape[:-1], gate_up.shape[-1] // 2))
+
+
+@torch.library.custom_op("mega_trading_amd::swiglu_packed_bwd", mutates_args=(), device_types="cuda")
+def swiglu_packed_bwd(gate_up: torch.Tensor, dout: torch.Tensor) -> torch.Tensor:
+    lib = _native.load()
+    gu, dy = _flat(gate_up), _flat(dout.to(gate_up.dtype))
+    cols = gu.shape[-1] // 2
+    rows = gu.numel() // max(2 * cols, 1)
+    dgu = torch.empty(gu.shape, device=gu.device, dtype=gu.dtype)
+    with torch.cuda.device(gu.device):
+        rc = lib.mt_swiglu_packed_bwd(gu.data_ptr(), dy.data_ptr(), dgu.data_ptr(), rows, cols, _DT[gu.dtype],
+                                      _stream(gu))
+    _native.check(rc, "mt_swiglu_packed_bwd")
+    return dgu
+
+
+@swiglu_packed_bwd.register_fake
+def _swiglu_packed_bwd_fake(gate_up, dout):
+    return torch.empty_like(gate_up, memory_format=torch.contiguous_format)
+
+
 _DTYPE_OF = {v: k for k, v in _DT.items()}
 # Logits bytes per chunk.  Measured at the C5 shape (32768 x 16384 bf16 logits,
 # fwd + bwd): 64 MB chunks (cache-resident) 3.8 ms, 256 MB 2.7 ms, one 1 GB
@@ -399,6 +449,18 @@ def _swiglu_backward(ctx, dout):
     return torch.ops.mega_trading_amd.swiglu_bwd(gate, up, dout)
 
 
+def _swiglu_packed_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+    ctx.set_materialize_grads(False)
+
+
+def _swiglu_packed_backward(ctx, dout):
+    (gate_up,) = ctx.saved_tensors
+    if dout is None:
+        return None
+    return torch.ops.mega_trading_amd.swiglu_packed_bwd(gate_up, dout)
+
+
 def _ce_setup(ctx, inputs, output):
     _h, _w, _labels, _ignore, _dt, need_grad = inputs
     _loss, gh, gw = output
@@ -419,3 +481,4 @@ rms_norm_fwd.register_autograd(_rms_backward, setup_context=_rms_setup)
 fused_linear_ce.register_autograd(_ce_backward, setup_context=_ce_setup)
 add_rms_norm_fwd.register_autograd(_add_rms_backward, setup_context=_add_rms_setup)
 swiglu_fwd.register_autograd(_swiglu_backward, setup_context=_swiglu_setup)
+swiglu_packed_fwd.register_autograd(_swiglu_packed_backward, setup_context=_swiglu_packed_setup)

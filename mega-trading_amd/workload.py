@@ -16,6 +16,7 @@ ends (``trainer.py:686-702``).
 
 from __future__ import annotations
 
+import gc
 import time
 
 import numpy as np
@@ -83,13 +84,25 @@ class TrainStep:
         return loss.detach()
 
     def tokens_per_second(self, steps: int, warmup: int) -> tuple[float, float, float]:
-        """(tokens/s, ms/step, last loss) over ``steps`` timed steps after ``warmup``."""
+        """(tokens/s, ms/step, last loss) over ``steps`` timed steps after ``warmup``.
+
+        The objects alive before the timed steps (about 270 k after importing
+        torch) are frozen out of the interpreter's cyclic garbage collector
+        for the duration: a full collection walks all of them (60-70 ms on
+        the GPU box, the length of several steps) and falls on an arbitrary
+        step, which a long training run amortises and a 20-step window does
+        not.  Every route is timed this way."""
         for _ in range(warmup):
             self()
         torch.cuda.synchronize(self.device)
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            loss = self()
-        torch.cuda.synchronize(self.device)
-        elapsed = time.perf_counter() - t0
+        gc.collect()
+        gc.freeze()
+        try:
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                loss = self()
+            torch.cuda.synchronize(self.device)
+            elapsed = time.perf_counter() - t0
+        finally:
+            gc.unfreeze()
         return self.labels.numel() * steps / elapsed, elapsed / steps * 1e3, float(loss)

@@ -178,6 +178,59 @@ def test_swiglu_matches_torch_eager_on_gpu(mta):
         torch.testing.assert_close(a.float(), b.float(), rtol=2 ** -7, atol=2 ** -7)
 
 
+@pytest.mark.parametrize("rows,cols,dt", [(32768, 1408, torch.bfloat16), (1, 8, torch.bfloat16), (333, 24, torch.float16),
+                                          (1000, 1408, torch.float32), (7, 704, torch.bfloat16)])
+def test_swiglu_packed_equals_the_pair_gate(rows, cols, dt):
+    # same kernel arithmetic on the packed (gate | up) rows: bit-identical to
+    # swiglu_gate on the two halves, forward and backward
+    from importlib import import_module
+    ops = import_module("mega-trading_amd.ops")
+    gu, dy = _gen((rows, 2 * cols), 21, dt, 3.0).cuda(), _gen((rows, cols), 22, dt).cuda()
+    a = gu.clone().requires_grad_(True)
+    out = ops.swiglu_gate_packed(a)
+    out.backward(dy)
+    g, u = gu[:, :cols].contiguous().requires_grad_(True), gu[:, cols:].contiguous().requires_grad_(True)
+    ref = ops.swiglu_gate(g, u)
+    ref.backward(dy)
+    torch.cuda.synchronize()
+    assert out.shape == (rows, cols) and out.dtype == dt
+    assert torch.equal(out, ref)
+    assert torch.equal(a.grad[:, :cols], g.grad) and torch.equal(a.grad[:, cols:], u.grad)
+
+
+def test_swiglu_packed_errors():
+    from importlib import import_module
+    ops = import_module("mega-trading_amd.ops")
+    with pytest.raises(ValueError, match="multiple of 8"):
+        ops.swiglu_gate_packed(torch.zeros(4, 24, device="cuda", dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("outs,rows", [((512, 128, 128), 32768), ((1408, 1408), 32768), ((512,), 32768),
+                                       ((64, 32), 1000), ((96,), 3 * 1024)])
+def test_projection_split_k_vs_fp64(outs, rows):
+    # bf16 autocast product (one GEMM over the stacked weights) and fp32 split-K
+    # weight gradients against fp64 products of the same bf16-rounded operands
+    from importlib import import_module
+    pj = import_module("mega-trading_amd.projection")
+    g = torch.Generator().manual_seed(rows + sum(outs))
+    x = torch.randn(rows, 512, generator=g).cuda().requires_grad_(True)
+    ws = [(torch.randn(o, 512, generator=g) * 0.02).cuda().requires_grad_(True) for o in outs]
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ys = pj.project(x, ws)
+    dys = [torch.randn(rows, o, generator=g).cuda().bfloat16() for o in outs]
+    torch.autograd.backward(ys, dys)
+    xb = x.detach().bfloat16().double()
+    for y, w, dy in zip(ys, ws, dys):
+        wb = w.detach().bfloat16().double()
+        assert y.dtype == torch.bfloat16 and w.grad.dtype == torch.float32
+        ref = xb @ wb.t()
+        assert ((y.double() - ref).norm() / ref.norm()).item() < 2 ** -8
+        ref_dw = dy.double().t() @ xb
+        assert ((w.grad.double() - ref_dw).norm() / ref_dw.norm()).item() < 1e-5  # fp32 accumulation
+    ref_dx = sum(dy.double() @ w.detach().bfloat16().double() for dy, w in zip(dys, ws))
+    assert ((x.grad.double() - ref_dx).norm() / ref_dx.norm()).item() < 2 ** -8
+
+
 def test_swiglu_errors(mta):
     with pytest.raises(ValueError, match="same shape"):
         mta.swiglu_gate(torch.zeros(4, device="cuda"), torch.zeros(5, device="cuda"))
