@@ -18,6 +18,9 @@
  *                           reached from triton_swiglu_gate :57-61 and
  *                           SwiGLU.forward, src/mega_trading/model.py:252-253
  *   mt_swiglu_bwd        <- _TritonSwiGLUGate.backward :455-474 (kernel :799-819)
+ *   mt_rms_norm_fwd_mixed, mt_add_rms_norm_fwd_mixed, mt_rms_norm_bwd_mixed
+ *                           no counterpart: the norms with an fp32 residual
+ *                           stream and 16-bit activations (autocast decoder)
  *   mt_swiglu_packed_fwd / _bwd  no counterpart: the same gate on the packed
  *                           output of one GEMM against the stacked (w1; w3)
  *                           weights (this build's "hip" decoder route)
@@ -79,6 +82,34 @@ int mt_rms_norm_bwd(const void* x, const void* weight, const float* rstd, const 
 int mt_add_rms_norm_bwd(const void* new_residual, const void* weight, const float* rstd, const void* d_new_residual,
                         const void* dy, void* dx, void* dweight, void* workspace, size_t workspace_bytes,
                         int64_t rows, int dim, int dtype, int weight_dtype, void* stream);
+
+/* Mixed-dtype forms for an autocast decoder: the residual stream (x of the
+ * plain norm, residual / new_residual of the add) and the weight are fp32,
+ * the activations (the branch output x of the add, y, dy) 16-bit
+ * (act_dtype bf16 or fp16).  y is the fp32 result rounded once to act_dtype:
+ * what the reference's fp32 norm followed by the next projection's autocast
+ * cast produces (model.py:184-187 with F.rms_norm, model.py:267-268), with
+ * the residual add of the block in front (new_residual = x + residual in
+ * fp32, as torch promotes it).  No counterpart in the reference's Triton
+ * operators (triton_ops.py:18-42 takes one dtype).
+ *
+ * mt_rms_norm_fwd_mixed: y = round(x * rstd * w), x fp32 (row stride), y act_dtype. */
+int mt_rms_norm_fwd_mixed(const void* x, int64_t x_row_stride, const void* weight, void* y, float* rstd, int64_t rows,
+                          int dim, float eps, int y_dtype, int weight_dtype, void* stream);
+
+/* new_residual = x + residual (fp32), y = round(RMSNorm(new_residual)); x act_dtype. */
+int mt_add_rms_norm_fwd_mixed(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                              const void* weight, void* new_residual, void* y, float* rstd, int64_t rows, int dim,
+                              float eps, int act_dtype, int weight_dtype, void* stream);
+
+/* Backward of both: s = the fp32 normalised input (x, or new_residual), dy
+ * act_dtype; ds (fp32) = the norm backward plus d_new_residual when that is
+ * not NULL; ds16, when not NULL, receives ds rounded to act_dtype (the
+ * gradient of the add's 16-bit branch input).  dweight fp32; workspace as
+ * for mt_rms_norm_bwd. */
+int mt_rms_norm_bwd_mixed(const void* s, const void* weight, const float* rstd, const void* d_new_residual,
+                          const void* dy, void* ds, void* ds16, void* dweight, void* workspace, size_t workspace_bytes,
+                          int64_t rows, int dim, int act_dtype, int weight_dtype, void* stream);
 
 /* out = round(silu(gate)) * up, silu(g) = g / (1 + exp(-g)). */
 int mt_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);

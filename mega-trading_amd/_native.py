@@ -33,6 +33,9 @@ EXPORTS = (
     "mt_rms_norm_bwd_workspace_size",
     "mt_rms_norm_bwd",
     "mt_add_rms_norm_bwd",
+    "mt_rms_norm_fwd_mixed",
+    "mt_add_rms_norm_fwd_mixed",
+    "mt_rms_norm_bwd_mixed",
     "mt_swiglu_fwd",
     "mt_swiglu_bwd",
     "mt_swiglu_packed_fwd",
@@ -60,6 +63,9 @@ _OPS_SIGNATURES = {
     "mt_rms_norm_bwd_workspace_size": (_S, [_L, _I]),
     "mt_rms_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
     "mt_add_rms_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
+    "mt_rms_norm_fwd_mixed": (_I, [_P, _L, _P, _P, _P, _L, _I, _F, _I, _I, _P]),
+    "mt_add_rms_norm_fwd_mixed": (_I, [_P, _L, _P, _L, _P, _P, _P, _P, _L, _I, _F, _I, _I, _P]),
+    "mt_rms_norm_bwd_mixed": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _L, _I, _I, _I, _P]),
     "mt_swiglu_fwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "mt_swiglu_bwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _P]),
     "mt_swiglu_packed_fwd": (_I, [_P, _P, _L, _L, _I, _P]),

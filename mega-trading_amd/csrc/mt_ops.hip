@@ -61,28 +61,77 @@ int bwd_blocks(int64_t rows) {
 }
 
 // ---- dispatch over (dtype, weight dtype, chunks) ---------------------------
-template <int DT, int WT, int NCH, bool ADD>
-hipError_t fwd_launch(const void* x, int64_t sx, const void* r, int64_t sr, const void* w, void* nr, void* y, float* rstd,
-                      int64_t rows, int dim, float eps, hipStream_t st) {
+// XT / ST / YT: storage of x, of the residual stream (residual, new residual)
+// and of y; one dtype for all of them in the reference operators.
+template <int XT, int ST, int YT, int WT, int NCH, bool ADD>
+hipError_t fwd_launch_x(const void* x, int64_t sx, const void* r, int64_t sr, const void* w, void* nr, void* y,
+                        float* rstd, int64_t rows, int dim, float eps, hipStream_t st) {
   const dim3 grid((unsigned)((rows + 3) / 4));
-  hipLaunchKernelGGL((K::rmsnorm_fwd_kernel<DT, WT, NCH, ADD>), grid, dim3(256), 0, st, x, sx, r, sr, w, nr, y, rstd,
-                     rows, dim, eps);
+  hipLaunchKernelGGL((K::rmsnorm_fwd_kernel<XT, ST, YT, WT, NCH, ADD>), grid, dim3(256), 0, st, x, sx, r, sr, w, nr, y,
+                     rstd, rows, dim, eps);
   return hipGetLastError();
 }
 
 template <int DT, int WT, int NCH, bool ADD>
-hipError_t bwd_launch(const void* s, const void* w, const float* rstd, const void* dy, const void* dres, void* ds,
-                      void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
+hipError_t fwd_launch(const void* x, int64_t sx, const void* r, int64_t sr, const void* w, void* nr, void* y, float* rstd,
+                      int64_t rows, int dim, float eps, hipStream_t st) {
+  return fwd_launch_x<DT, DT, DT, WT, NCH, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+}
+
+// ST: storage of s, d_new_res and ds; GT: of dy (and of the optional ds16 copy)
+template <int ST, int GT, int WT, int NCH, bool ADD>
+hipError_t bwd_launch_x(const void* s, const void* w, const float* rstd, const void* dy, const void* dres, void* ds,
+                        void* ds16, void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
   const int nb = bwd_blocks(rows);
   if (rows > 0) {
-    hipLaunchKernelGGL((K::rmsnorm_bwd_kernel<DT, WT, NCH, ADD>), dim3(nb), dim3(256), 0, st, s, w, rstd, dy, dres, ds,
-                       partial, rows, dim);
+    hipLaunchKernelGGL((K::rmsnorm_bwd_kernel<ST, GT, WT, NCH, ADD>), dim3(nb), dim3(256), 0, st, s, w, rstd, dy, dres,
+                       ds, ds16, partial, rows, dim);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((K::column_sum_kernel<WT>), dim3((dim + 63) / 64), dim3(64 * K::kColWaves), 0, st, partial,
                      rows > 0 ? nb : 0, dim, dw);
   return hipGetLastError();
+}
+
+template <int DT, int WT, int NCH, bool ADD>
+hipError_t bwd_launch(const void* s, const void* w, const float* rstd, const void* dy, const void* dres, void* ds,
+                      void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
+  return bwd_launch_x<DT, DT, WT, NCH, ADD>(s, w, rstd, dy, dres, ds, nullptr, dw, partial, rows, dim, st);
+}
+
+// ---- mixed form: fp32 residual stream and weight, 16-bit activations (AT) --
+template <int AT, bool ADD>
+hipError_t fwd_mixed(int nch, const void* x, int64_t sx, const void* r, int64_t sr, const void* w, void* nr, void* y,
+                     float* rstd, int64_t rows, int dim, float eps, hipStream_t st) {
+  // x: the 16-bit branch output when ADD, else the fp32 residual stream itself
+  constexpr int XT = ADD ? AT : K::kDtFP32;
+  constexpr int F = K::kDtFP32;
+  switch (nch) {
+    case 1: return fwd_launch_x<XT, F, AT, F, 1, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    case 2: return fwd_launch_x<XT, F, AT, F, 2, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    case 4: return fwd_launch_x<XT, F, AT, F, 4, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+    default: return fwd_launch_x<XT, F, AT, F, 8, ADD>(x, sx, r, sr, w, nr, y, rstd, rows, dim, eps, st);
+  }
+}
+
+template <int AT, bool ADD>
+hipError_t bwd_mixed(int nch, const void* s, const void* w, const float* rstd, const void* dy, const void* dres,
+                     void* ds, void* ds16, void* dw, float* partial, int64_t rows, int dim, hipStream_t st) {
+  constexpr int F = K::kDtFP32;
+  switch (nch) {
+    case 1: return bwd_launch_x<F, AT, F, 1, ADD>(s, w, rstd, dy, dres, ds, ds16, dw, partial, rows, dim, st);
+    case 2: return bwd_launch_x<F, AT, F, 2, ADD>(s, w, rstd, dy, dres, ds, ds16, dw, partial, rows, dim, st);
+    case 4: return bwd_launch_x<F, AT, F, 4, ADD>(s, w, rstd, dy, dres, ds, ds16, dw, partial, rows, dim, st);
+    default: return bwd_launch_x<F, AT, F, 8, ADD>(s, w, rstd, dy, dres, ds, ds16, dw, partial, rows, dim, st);
+  }
+}
+
+int check_mixed(int act_dtype, int weight_dtype) {
+  if (act_dtype != MT_DTYPE_BF16 && act_dtype != MT_DTYPE_FP16)
+    return fail(MT_E_DTYPE, "activation dtype code %d unsupported (bf16 or fp16)", act_dtype);
+  if (weight_dtype != MT_DTYPE_FP32) return fail(MT_E_DTYPE, "weight dtype code %d must be fp32", weight_dtype);
+  return MT_OK;
 }
 
 template <int DT, int WT, bool ADD>
@@ -236,6 +285,78 @@ int mt_add_rms_norm_bwd(const void* new_residual, const void* weight, const floa
   if (rows > 0 && (rc = check_ptr("d_new_residual", d_new_residual))) return rc;
   const hipError_t e = bwd_dispatch<true>(dtype, weight_dtype, new_residual, weight, rstd, dy, d_new_residual, dx,
                                           dweight, static_cast<float*>(workspace), rows, dim, (hipStream_t)stream);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_rms_norm_fwd_mixed(const void* x, int64_t x_row_stride, const void* weight, void* y, float* rstd, int64_t rows,
+                          int dim, float eps, int y_dtype, int weight_dtype, void* stream) {
+  int rc;
+  if ((rc = check_mixed(y_dtype, weight_dtype)) || (rc = check_rows(rows, dim))) return rc;
+  if ((rc = check_ptr("weight", weight))) return rc;
+  if (rows == 0) return ok();
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("y", y)) || (rc = check_stride("x", x_row_stride, dim))) return rc;
+  if (!rstd) return fail(MT_E_NULL, "rstd is NULL");
+  const int n = chunks(dim);
+  hipStream_t st = (hipStream_t)stream;
+  const hipError_t e =
+      y_dtype == MT_DTYPE_BF16
+          ? fwd_mixed<K::kDtBF16, false>(n, x, x_row_stride, nullptr, 0, weight, nullptr, y, rstd, rows, dim, eps, st)
+          : fwd_mixed<K::kDtFP16, false>(n, x, x_row_stride, nullptr, 0, weight, nullptr, y, rstd, rows, dim, eps, st);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_add_rms_norm_fwd_mixed(const void* x, int64_t x_row_stride, const void* residual, int64_t residual_row_stride,
+                              const void* weight, void* new_residual, void* y, float* rstd, int64_t rows, int dim,
+                              float eps, int act_dtype, int weight_dtype, void* stream) {
+  int rc;
+  if ((rc = check_mixed(act_dtype, weight_dtype)) || (rc = check_rows(rows, dim))) return rc;
+  if ((rc = check_ptr("weight", weight))) return rc;
+  if (rows == 0) return ok();
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("residual", residual)) ||
+      (rc = check_ptr("new_residual", new_residual)) || (rc = check_ptr("y", y)) ||
+      (rc = check_stride("x", x_row_stride, dim)) || (rc = check_stride("residual", residual_row_stride, dim)))
+    return rc;
+  if (!rstd) return fail(MT_E_NULL, "rstd is NULL");
+  const int n = chunks(dim);
+  hipStream_t st = (hipStream_t)stream;
+  const hipError_t e =
+      act_dtype == MT_DTYPE_BF16
+          ? fwd_mixed<K::kDtBF16, true>(n, x, x_row_stride, residual, residual_row_stride, weight, new_residual, y,
+                                        rstd, rows, dim, eps, st)
+          : fwd_mixed<K::kDtFP16, true>(n, x, x_row_stride, residual, residual_row_stride, weight, new_residual, y,
+                                        rstd, rows, dim, eps, st);
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_rms_norm_bwd_mixed(const void* s, const void* weight, const float* rstd, const void* d_new_residual,
+                          const void* dy, void* ds, void* ds16, void* dweight, void* workspace, size_t workspace_bytes,
+                          int64_t rows, int dim, int act_dtype, int weight_dtype, void* stream) {
+  int rc;
+  if ((rc = check_mixed(act_dtype, weight_dtype)) || (rc = check_rows(rows, dim))) return rc;
+  if ((rc = check_ptr("weight", weight)) || (rc = check_ptr("dweight", dweight)) ||
+      (rc = check_ptr("workspace", workspace)))
+    return rc;
+  if (rows > 0) {
+    if ((rc = check_ptr("s", s)) || (rc = check_ptr("dy", dy)) || (rc = check_ptr("ds", ds))) return rc;
+    if (d_new_residual && (rc = check_ptr("d_new_residual", d_new_residual))) return rc;
+    if (ds16 && (rc = check_ptr("ds16", ds16))) return rc;
+    if (!rstd) return fail(MT_E_NULL, "rstd is NULL");
+  }
+  if (workspace_bytes < mt_rms_norm_bwd_workspace_size(rows, dim))
+    return fail(MT_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                mt_rms_norm_bwd_workspace_size(rows, dim));
+  const int n = chunks(dim);
+  hipStream_t st = (hipStream_t)stream;
+  float* part = static_cast<float*>(workspace);
+  hipError_t e;
+  if (act_dtype == MT_DTYPE_BF16)
+    e = d_new_residual
+            ? bwd_mixed<K::kDtBF16, true>(n, s, weight, rstd, dy, d_new_residual, ds, ds16, dweight, part, rows, dim, st)
+            : bwd_mixed<K::kDtBF16, false>(n, s, weight, rstd, dy, nullptr, ds, ds16, dweight, part, rows, dim, st);
+  else
+    e = d_new_residual
+            ? bwd_mixed<K::kDtFP16, true>(n, s, weight, rstd, dy, d_new_residual, ds, ds16, dweight, part, rows, dim, st)
+            : bwd_mixed<K::kDtFP16, false>(n, s, weight, rstd, dy, nullptr, ds, ds16, dweight, part, rows, dim, st);
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }
 

@@ -94,12 +94,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // ===========================================================================
 // RMSNorm forward (ADD: the residual add fused in front)
-//   ADD:  s = x + r (fp32), new_res = s (stored in DT), y = s * rstd * w
+//   ADD:  s = x + r (fp32), new_res = s (stored in ST), y = s * rstd * w
 //   else: y = x * rstd * w
 //   rstd = 1 / sqrt(mean(s^2) + eps) (fp32, one per row)
+// Storage types: x in XT, residual and new_res in ST, y in YT.  One dtype for
+// all of them is the reference operator; the mixed form (x and y 16-bit, the
+// residual stream fp32) is the autocast decoder's residual add followed by
+// the next norm, whose output the next projection reads in 16 bits anyway.
 // One wave per row; lane L holds chunks L, L + 64, ... (8 values each).
 // ===========================================================================
-template <int DT, int WT, int NCH, bool ADD>
+template <int XT, int ST, int YT, int WT, int NCH, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const void* x, int64_t sx, const void* res, int64_t sr,
                                                           const void* w, void* new_res, void* y, float* rstd,
                                                           int64_t rows, int D, float eps) {
@@ -114,13 +118,13 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const void* x, int64_t
   for (int k = 0; k < NCH; ++k) {
     const int c = lane + 64 * k;
     if (c < nch) {
-      IO<DT>::load8(x, row * sx + 8 * c, v[k]);
+      IO<XT>::load8(x, row * sx + 8 * c, v[k]);
       if constexpr (ADD) {
         float r[8];
-        IO<DT>::load8(res, row * sr + 8 * c, r);
+        IO<ST>::load8(res, row * sr + 8 * c, r);
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[k][j] += r[j];
-        IO<DT>::store8(new_res, row * D + 8 * c, v[k]);
+        IO<ST>::store8(new_res, row * D + 8 * c, v[k]);
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += v[k][j] * v[k][j];
@@ -136,24 +140,25 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const void* x, int64_t
       IO<WT>::load8(w, 8 * c, wv);
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = v[k][j] * inv * wv[j];
-      IO<DT>::store8(y, row * D + 8 * c, o);
+      IO<YT>::store8(y, row * D + 8 * c, o);
     }
   }
   if (lane == 0) rstd[row] = inv;
 }
 
 // ===========================================================================
-// RMSNorm backward (dy and ds in the storage type of s).  With g = dy * w
-// (fp32) and c = sum(g * s) over the row:
+// RMSNorm backward.  With g = dy * w (fp32) and c = sum(g * s) over the row:
 //   ds = rstd * (g - s * rstd^2 / D * c)        (+ d_new_res when ADD)
 //   dw = sum over rows of dy * s * rstd         (per-workgroup partial sums)
-// s is x (or the stored new residual when ADD).  Waves stride over rows; each
-// lane accumulates its dw chunks in registers, the 4 waves of a workgroup
-// combine them in LDS and write one fp32 partial row per workgroup.
+// s is x (or the stored new residual when ADD).  s, d_new_res and ds in ST,
+// dy in GT; when ds16 is not null ds is also written there in GT (the
+// gradient of a 16-bit branch input of the mixed add).  Waves stride over
+// rows; each lane accumulates its dw chunks in registers, the 4 waves of a
+// workgroup combine them in LDS and write one fp32 partial row per workgroup.
 // ===========================================================================
-template <int DT, int WT, int NCH, bool ADD>
+template <int ST, int GT, int WT, int NCH, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const void* s, const void* w, const float* rstd,
-                                                          const void* dy, const void* dres, void* ds,
+                                                          const void* dy, const void* dres, void* ds, void* ds16,
                                                           float* partial, int64_t rows, int D) {
   __shared__ float red[3][NCH * 512];
   const int wave = threadIdx.x >> 6;
@@ -183,8 +188,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const void* s, const v
         for (int k = 0; k < NCH; ++k) {
           const int c = lane + 64 * k;
           if (c < nch) {
-            IO<DT>::load8(s, row * D + 8 * c, sv[u][k]);
-            IO<DT>::load8(dy, row * D + 8 * c, g[u][k]);
+            IO<ST>::load8(s, row * D + 8 * c, sv[u][k]);
+            IO<GT>::load8(dy, row * D + 8 * c, g[u][k]);
           }
         }
       }
@@ -217,11 +222,12 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const void* s, const v
           for (int j = 0; j < 8; ++j) o[j] = r[u] * (g[u][k][j] - sv[u][k][j] * f);
           if constexpr (ADD) {
             float dr[8];
-            IO<DT>::load8(dres, row * D + 8 * c, dr);
+            IO<ST>::load8(dres, row * D + 8 * c, dr);
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] += dr[j];
           }
-          IO<DT>::store8(ds, row * D + 8 * c, o);
+          IO<ST>::store8(ds, row * D + 8 * c, o);
+          if (ds16) IO<GT>::store8(ds16, row * D + 8 * c, o);
         }
       }
     }

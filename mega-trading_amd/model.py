@@ -41,7 +41,9 @@ from .attention import decode_attention as _hip_decode_attention
 from .attention import decode_rope_append as _hip_decode_rope_append
 from .attention import rope_attention as _hip_rope_attention
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
+from .ops import add_rms_norm_mixed as _hip_add_rms_norm_mixed
 from .ops import rms_norm as _hip_rms_norm
+from .ops import rms_norm_mixed as _hip_rms_norm_mixed
 from .ops import swiglu_gate as _hip_swiglu_gate
 from .ops import swiglu_gate_packed as _hip_swiglu_gate_packed
 from .projection import project as _project
@@ -223,9 +225,34 @@ class TradingModel(nn.Module):
         if input_ids.shape[1] > self.block_size:
             raise ValueError(f"sequence length {input_ids.shape[1]} exceeds block_size {self.block_size}")
         hidden = self.token_embedding(input_ids)
+        if self._fused_norms(hidden):
+            return self._hidden_fused(hidden)
         for block in self.blocks:
             hidden = block(hidden)
         return self.norm(hidden)
+
+    def _fused_norms(self, hidden: torch.Tensor) -> bool:
+        """The "hip" route under 16-bit CUDA autocast with an fp32 residual stream."""
+        return (self.operator_backend == "hip" and hidden.is_cuda and hidden.dtype == torch.float32
+                and torch.is_autocast_enabled("cuda")
+                and torch.get_autocast_dtype("cuda") in (torch.bfloat16, torch.float16)
+                and self.norm.weight.dtype == torch.float32)
+
+    def _hidden_fused(self, hidden: torch.Tensor) -> torch.Tensor:
+        """The blocks of ``_hidden`` (``model.py:184-187`` each) with every
+        residual add fused into the RMSNorm that reads its sum: the next
+        block's attention norm, the block's FFN norm, or the final norm.  The
+        norms write the autocast dtype that the following projection would
+        cast to; the residual stream stays fp32 (``ops.add_rms_norm_mixed``)."""
+        act = torch.get_autocast_dtype("cuda")
+        first = self.blocks[0].attention_norm if len(self.blocks) else self.norm
+        normed = _hip_rms_norm_mixed(hidden, first.weight, eps=first.eps, out_dtype=act)
+        for i, block in enumerate(self.blocks):
+            nxt = self.blocks[i + 1].attention_norm if i + 1 < len(self.blocks) else self.norm
+            ffn_norm = block.ffn_norm
+            hidden, normed = _hip_add_rms_norm_mixed(block.attention(normed), hidden, ffn_norm.weight, eps=ffn_norm.eps)
+            hidden, normed = _hip_add_rms_norm_mixed(block.feed_forward(normed), hidden, nxt.weight, eps=nxt.eps)
+        return normed
 
 
 class LlamaDecoderBlock(nn.Module):

@@ -21,15 +21,18 @@ registered backward, launched on the caller's current stream.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 
 from . import _native
 
-__all__ = ["rms_norm", "add_rms_norm", "swiglu_gate", "swiglu_gate_packed", "fused_linear_cross_entropy",
-           "MAX_NORM_DIM"]
+__all__ = ["rms_norm", "add_rms_norm", "rms_norm_mixed", "add_rms_norm_mixed", "swiglu_gate", "swiglu_gate_packed",
+           "fused_linear_cross_entropy", "MAX_NORM_DIM"]
 
 MAX_NORM_DIM = 4096
 _DT = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16, torch.float32: _native.DTYPE_FP32}
+_DTYPE_OF = {v: k for k, v in _DT.items()}
 
 
 # ---------------------------------------------------------------------------
@@ -53,6 +56,33 @@ def add_rms_norm(
     if residual.dtype != hidden.dtype or residual.device != hidden.device:
         raise RuntimeError("residual must have the dtype and device of hidden")
     new_res, y, _rstd = torch.ops.mega_trading_amd.add_rms_norm_fwd(hidden, residual, weight, float(eps))
+    return new_res, y
+
+
+def rms_norm_mixed(hidden: torch.Tensor, weight: torch.Tensor, *, eps: float, out_dtype: torch.dtype) -> torch.Tensor:
+    """``rms_norm`` of an fp32 residual stream with the result rounded once to
+    the 16-bit ``out_dtype``: what the fp32 norm followed by the next
+    projection's autocast cast gives, in one pass.  ``weight`` fp32."""
+    _check_norm(hidden, weight)
+    _check_mixed(hidden, weight, out_dtype)
+    y, _rstd = torch.ops.mega_trading_amd.rms_norm_fwd_mixed(hidden, weight, float(eps), _DT[out_dtype])
+    return y
+
+
+def add_rms_norm_mixed(
+    branch: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, *, eps: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(new_residual, normed)``: ``new_residual = residual + branch`` in fp32
+    (torch's promotion of an fp32 residual stream plus a 16-bit branch output)
+    and ``normed = RMSNorm(new_residual)`` rounded once to the branch's dtype.
+    ``residual`` and ``weight`` fp32, ``branch`` bf16 or fp16."""
+    _check_norm(residual, weight)
+    _check_mixed(residual, weight, branch.dtype)
+    if branch.shape != residual.shape:
+        raise ValueError("branch must have the shape of residual")
+    if branch.device != residual.device:
+        raise RuntimeError("branch must be on the device of residual")
+    new_res, y, _rstd = torch.ops.mega_trading_amd.add_rms_norm_fwd_mixed(branch, residual, weight, float(eps))
     return new_res, y
 
 
@@ -139,6 +169,13 @@ def _check_norm(hidden: torch.Tensor, weight: torch.Tensor) -> None:
         raise RuntimeError("weight must be on the device of hidden")
 
 
+def _check_mixed(stream: torch.Tensor, weight: torch.Tensor, act: torch.dtype) -> None:
+    if stream.dtype != torch.float32 or weight.dtype != torch.float32:
+        raise RuntimeError("the residual stream and the weight must be float32")
+    if act not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"activation dtype {act} unsupported (bfloat16 or float16)")
+
+
 def _rows(x: torch.Tensor) -> tuple[torch.Tensor, int]:
     """[..., D] -> ([rows, D] usable in place or a contiguous copy, row stride)."""
     d = x.shape[-1]
@@ -160,6 +197,10 @@ def _weight(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     if w.dtype != x.dtype and w.dtype != torch.float32:
         w = w.to(torch.float32)
     return _flat(w)
+
+
+def _ptr_or_none(t: Optional[torch.Tensor]) -> Optional[int]:
+    return t.data_ptr() if t is not None else None
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -270,6 +311,88 @@ def _norm_bwd(s, weight, rstd, dy, dres):
     return dx.view(s.shape), dw.to(weight.dtype)
 
 
+@torch.library.custom_op("mega_trading_amd::rms_norm_fwd_mixed", mutates_args=(), device_types="cuda")
+def rms_norm_fwd_mixed(x: torch.Tensor, weight: torch.Tensor, eps: float, act: int
+                       ) -> tuple[torch.Tensor, torch.Tensor]:
+    """x fp32 -> (y in the 16-bit dtype of code ``act``, rstd fp32 [rows])."""
+    lib = _native.load()
+    x2, sx = _rows(x)
+    w = _flat(weight)
+    rows, d = x2.shape
+    y = torch.empty((rows, d), device=x.device, dtype=_DTYPE_OF[act])
+    rstd = torch.empty((rows,), device=x.device, dtype=torch.float32)
+    with torch.cuda.device(x.device):
+        rc = lib.mt_rms_norm_fwd_mixed(x2.data_ptr(), sx, w.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, d, eps,
+                                       act, _DT[w.dtype], _stream(x))
+    _native.check(rc, "mt_rms_norm_fwd_mixed")
+    return y.view(x.shape), rstd
+
+
+@rms_norm_fwd_mixed.register_fake
+def _rms_norm_fwd_mixed_fake(x, weight, eps, act):
+    return x.new_empty(x.shape, dtype=_DTYPE_OF[act]), x.new_empty((x.numel() // max(x.shape[-1], 1),),
+                                                                  dtype=torch.float32)
+
+
+@torch.library.custom_op("mega_trading_amd::add_rms_norm_fwd_mixed", mutates_args=(), device_types="cuda")
+def add_rms_norm_fwd_mixed(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float
+                           ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x 16-bit, residual fp32 -> (new_residual fp32, y in x's dtype, rstd)."""
+    lib = _native.load()
+    x2, sx = _rows(x)
+    r2, sr = _rows(residual)
+    w = _flat(weight)
+    rows, d = x2.shape
+    new_res = torch.empty((rows, d), device=x.device, dtype=torch.float32)
+    y = torch.empty((rows, d), device=x.device, dtype=x.dtype)
+    rstd = torch.empty((rows,), device=x.device, dtype=torch.float32)
+    with torch.cuda.device(x.device):
+        rc = lib.mt_add_rms_norm_fwd_mixed(x2.data_ptr(), sx, r2.data_ptr(), sr, w.data_ptr(), new_res.data_ptr(),
+                                           y.data_ptr(), rstd.data_ptr(), rows, d, eps, _DT[x.dtype], _DT[w.dtype],
+                                           _stream(x))
+    _native.check(rc, "mt_add_rms_norm_fwd_mixed")
+    return new_res.view(x.shape), y.view(x.shape), rstd
+
+
+@add_rms_norm_fwd_mixed.register_fake
+def _add_rms_norm_fwd_mixed_fake(x, residual, weight, eps):
+    rows = x.numel() // max(x.shape[-1], 1)
+    return (x.new_empty(x.shape, dtype=torch.float32), x.new_empty(x.shape),
+            x.new_empty((rows,), dtype=torch.float32))
+
+
+@torch.library.custom_op("mega_trading_amd::rms_norm_bwd_mixed", mutates_args=(), device_types="cuda")
+def rms_norm_bwd_mixed(s: torch.Tensor, weight: torch.Tensor, rstd: torch.Tensor, d_new_residual: Optional[torch.Tensor],
+                       dy: torch.Tensor, act: int, want16: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(ds fp32 [+ d_new_residual], ds rounded to ``act`` when ``want16`` (else
+    an empty tensor), dweight fp32) for s fp32 and dy 16-bit."""
+    lib = _native.load()
+    d = s.shape[-1]
+    s2 = _flat(s.reshape(-1, d))
+    dy2 = _flat(dy.to(_DTYPE_OF[act]).reshape(-1, d))
+    dr2 = _flat(d_new_residual.to(torch.float32).reshape(-1, d)) if d_new_residual is not None else None
+    w = _flat(weight)
+    rows = s2.shape[0]
+    ds = torch.empty((rows, d), device=s.device, dtype=torch.float32)
+    ds16 = torch.empty((rows, d) if want16 else (0,), device=s.device, dtype=_DTYPE_OF[act])
+    dw = torch.empty((d,), device=s.device, dtype=torch.float32)
+    with torch.cuda.device(s.device):
+        ws_bytes = lib.mt_rms_norm_bwd_workspace_size(rows, d)
+        ws = torch.empty(max(ws_bytes, 256), device=s.device, dtype=torch.uint8)
+        rc = lib.mt_rms_norm_bwd_mixed(s2.data_ptr(), w.data_ptr(), rstd.data_ptr(), _ptr_or_none(dr2),
+                                       dy2.data_ptr(), ds.data_ptr(), ds16.data_ptr() if want16 else None,
+                                       dw.data_ptr(), ws.data_ptr(), ws.numel(), rows, d, act, _DT[w.dtype],
+                                       _stream(s))
+    _native.check(rc, "mt_rms_norm_bwd_mixed")
+    return ds.view(s.shape), (ds16.view(s.shape) if want16 else ds16), dw
+
+
+@rms_norm_bwd_mixed.register_fake
+def _rms_norm_bwd_mixed_fake(s, weight, rstd, d_new_residual, dy, act, want16):
+    return (s.new_empty(s.shape, dtype=torch.float32),
+            s.new_empty(s.shape if want16 else (0,), dtype=_DTYPE_OF[act]), torch.empty_like(weight))
+
+
 @torch.library.custom_op("mega_trading_amd::swiglu_fwd", mutates_args=(), device_types="cuda")
 def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     lib = _native.load()
@@ -342,7 +465,6 @@ def _swiglu_packed_bwd_fake(gate_up, dout):
     return torch.empty_like(gate_up, memory_format=torch.contiguous_format)
 
 
-_DTYPE_OF = {v: k for k, v in _DT.items()}
 # Logits bytes per chunk.  Measured at the C5 shape (32768 x 16384 bf16 logits,
 # fwd + bwd): 64 MB chunks (cache-resident) 3.8 ms, 256 MB 2.7 ms, one 1 GB
 # chunk 2.3 ms (the three GEMMs alone take 1.6 ms), against 4.4 ms for the eager
@@ -436,6 +558,41 @@ def _add_rms_backward(ctx, d_new_res, dy, _drstd):
     return dx, dx, dw, None
 
 
+def _rms_mixed_setup(ctx, inputs, output):
+    x, weight, _eps, act = inputs
+    _y, rstd = output
+    ctx.act = act
+    ctx.save_for_backward(x, weight, rstd)
+    ctx.set_materialize_grads(False)
+
+
+def _rms_mixed_backward(ctx, dy, _drstd):
+    x, weight, rstd = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None
+    dx, _ds16, dw = torch.ops.mega_trading_amd.rms_norm_bwd_mixed(x, weight, rstd, None, dy, ctx.act, False)
+    return dx, dw, None, None
+
+
+def _add_rms_mixed_setup(ctx, inputs, output):
+    x, _residual, weight, _eps = inputs
+    new_res, _y, rstd = output
+    ctx.act = _DT[x.dtype]
+    ctx.save_for_backward(new_res, weight, rstd)
+    ctx.set_materialize_grads(False)
+
+
+def _add_rms_mixed_backward(ctx, d_new_res, dy, _drstd):
+    new_res, weight, rstd = ctx.saved_tensors
+    if dy is None:
+        if d_new_res is None:
+            return None, None, None, None
+        # only the sum is used: both inputs get its gradient (in their dtypes)
+        return d_new_res.to(_DTYPE_OF[ctx.act]), d_new_res, None, None
+    ds, ds16, dw = torch.ops.mega_trading_amd.rms_norm_bwd_mixed(new_res, weight, rstd, d_new_res, dy, ctx.act, True)
+    return ds16, ds, dw, None
+
+
 def _swiglu_setup(ctx, inputs, output):
     gate, up = inputs
     ctx.save_for_backward(gate, up)
@@ -482,3 +639,5 @@ fused_linear_ce.register_autograd(_ce_backward, setup_context=_ce_setup)
 add_rms_norm_fwd.register_autograd(_add_rms_backward, setup_context=_add_rms_setup)
 swiglu_fwd.register_autograd(_swiglu_backward, setup_context=_swiglu_setup)
 swiglu_packed_fwd.register_autograd(_swiglu_packed_backward, setup_context=_swiglu_packed_setup)
+rms_norm_fwd_mixed.register_autograd(_rms_mixed_backward, setup_context=_rms_mixed_setup)
+add_rms_norm_fwd_mixed.register_autograd(_add_rms_mixed_backward, setup_context=_add_rms_mixed_setup)

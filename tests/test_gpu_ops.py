@@ -178,6 +178,55 @@ def test_swiglu_matches_torch_eager_on_gpu(mta):
         torch.testing.assert_close(a.float(), b.float(), rtol=2 ** -7, atol=2 ** -7)
 
 
+@pytest.mark.parametrize("rows,d,act", [(32768, 512, torch.bfloat16), (1, 8, torch.bfloat16), (333, 1024, torch.float16),
+                                        (77, 4096, torch.bfloat16), (5, 24, torch.float16)])
+def test_mixed_norms_equal_the_fp32_kernels_rounded(mta, rows, d, act):
+    # fp32 residual stream + 16-bit activations: the same fp32 arithmetic as the
+    # single-dtype fp32 kernels, with the 16-bit outputs rounded once
+    from importlib import import_module
+    ops = import_module("mega-trading_amd.ops")
+    branch = _gen((rows, d), 31, act).cuda()
+    res = _gen((rows, d), 32, torch.float32).cuda()
+    w = (1.0 + 0.1 * _gen((d,), 33, torch.float32)).cuda()
+    dy = _gen((rows, d), 34, act).cuda()
+    dres = _gen((rows, d), 35, torch.float32).cuda()
+    # add + norm
+    a_b, a_r, a_w = (t.clone().requires_grad_(True) for t in (branch, res, w))
+    new_a, y_a = ops.add_rms_norm_mixed(a_b, a_r, a_w, eps=1e-5)
+    torch.autograd.backward((new_a, y_a), (dres, dy))
+    b_b, b_r, b_w = branch.float().requires_grad_(True), res.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    new_b, y_b = mta.add_rms_norm(b_b, b_r, b_w, eps=1e-5)
+    torch.autograd.backward((new_b, y_b), (dres, dy.float()))
+    torch.cuda.synchronize()
+    assert new_a.dtype == torch.float32 and y_a.dtype == act and a_b.grad.dtype == act
+    assert torch.equal(new_a, new_b) and torch.equal(y_a, y_b.to(act))
+    assert torch.equal(a_r.grad, b_r.grad) and torch.equal(a_b.grad, b_b.grad.to(act))
+    assert torch.equal(a_w.grad, b_w.grad)
+    # plain norm of the fp32 stream
+    c_x, c_w = res.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    y_c = ops.rms_norm_mixed(c_x, c_w, eps=1e-5, out_dtype=act)
+    y_c.backward(dy)
+    d_x, d_w = res.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    y_d = mta.rms_norm(d_x, d_w, eps=1e-5)
+    y_d.backward(dy.float())
+    torch.cuda.synchronize()
+    assert y_c.dtype == act and torch.equal(y_c, y_d.to(act))
+    assert torch.equal(c_x.grad, d_x.grad) and torch.equal(c_w.grad, d_w.grad)
+
+
+def test_mixed_norm_errors():
+    from importlib import import_module
+    ops = import_module("mega-trading_amd.ops")
+    x = torch.zeros(4, 16, device="cuda")
+    w = torch.ones(16, device="cuda")
+    with pytest.raises(RuntimeError, match="float32"):
+        ops.rms_norm_mixed(x.bfloat16(), w, eps=1e-5, out_dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="unsupported"):
+        ops.rms_norm_mixed(x, w, eps=1e-5, out_dtype=torch.float32)
+    with pytest.raises(ValueError, match="shape"):
+        ops.add_rms_norm_mixed(torch.zeros(2, 16, device="cuda", dtype=torch.bfloat16), x, w, eps=1e-5)
+
+
 @pytest.mark.parametrize("rows,cols,dt", [(32768, 1408, torch.bfloat16), (1, 8, torch.bfloat16), (333, 24, torch.float16),
                                           (1000, 1408, torch.float32), (7, 704, torch.bfloat16)])
 def test_swiglu_packed_equals_the_pair_gate(rows, cols, dt):
