@@ -25,8 +25,8 @@ import torch
 
 from . import _native
 
-__all__ = ["attention", "rope_attention", "attention_forward", "decode_attention", "SUPPORTED_HEAD_DIMS",
-           "MAX_DECODE_REPEATS"]
+__all__ = ["attention", "rope_attention", "rope_attention_packed", "attention_forward", "decode_attention",
+           "SUPPORTED_HEAD_DIMS", "MAX_DECODE_REPEATS"]
 
 MAX_DECODE_REPEATS = 8
 
@@ -71,6 +71,45 @@ def rope_attention(
     c, s = _rope_tables(cos, sin, query)
     out, _lse = _forward(query, key, value, c, s)
     return out
+
+
+def rope_attention_packed(
+    qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, heads: int, kv_heads: int
+) -> torch.Tensor:
+    """``rope_attention`` on the packed output of one q|k|v projection GEMM.
+
+    ``qkv`` [B, T, (heads + 2 kv_heads) * D] holds, per token, the query
+    heads, then the key heads, then the value heads (``model.py:220-222``'s
+    three products side by side), bf16 or fp16.  Returns the attention output
+    as [B, T, heads * D], the layout the output projection reads
+    (``model.py:236``), written there directly by the kernel; the backward
+    writes dQ, dK and dV into one gradient of qkv's layout.  Results equal
+    ``rope_attention`` on the three head views."""
+    if qkv.ndim != 3:
+        raise ValueError("qkv must have shape [batch, time, (heads + 2 kv_heads) * head_dim]")
+    if heads <= 0 or kv_heads <= 0 or heads % kv_heads:
+        raise ValueError("heads must be a positive multiple of kv_heads")
+    if qkv.shape[-1] % (heads + 2 * kv_heads):
+        raise ValueError("qkv's last dim must be (heads + 2 kv_heads) * head_dim")
+    if qkv.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"qkv dtype {qkv.dtype} unsupported (bfloat16 or float16)")
+    q, k, v = _packed_views(qkv, heads, kv_heads)
+    _validate(q, k, v, heads // kv_heads)
+    c, s = _rope_tables(cos, sin, q)
+    d = q.shape[-1]
+    out, _lse, _q_rot, _k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_packed_fwd(
+        qkv, c, s, heads, kv_heads, 1.0 / math.sqrt(d))
+    return out
+
+
+def _packed_views(qkv: torch.Tensor, heads: int, kv_heads: int):
+    """[B, H, T, D] views of the query, key and value heads of a packed qkv."""
+    b, t, width = qkv.shape
+    d = width // (heads + 2 * kv_heads)
+    q = qkv[..., : heads * d].view(b, t, heads, d).transpose(1, 2)
+    k = qkv[..., heads * d:(heads + kv_heads) * d].view(b, t, kv_heads, d).transpose(1, 2)
+    v = qkv[..., (heads + kv_heads) * d:].view(b, t, kv_heads, d).transpose(1, 2)
+    return q, k, v
 
 
 def attention_forward(
@@ -239,12 +278,13 @@ def _forward(q, k, v, cos, sin):
     return out, lse
 
 
-def _launch_fwd(q, k, v, cos, sin, scale):
+def _launch_fwd(q, k, v, cos, sin, scale, out=None):
     lib = _native.load()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     b, hq, t, d = q.shape
     hkv = k.shape[1]
-    out = _kernel_ready(torch.empty_like(q))
+    if out is None:
+        out = _kernel_ready(torch.empty_like(q))
     lse = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
     q_rot = k_rot = None
     if cos is not None:
@@ -308,15 +348,23 @@ def gqa_attn_bwd(
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients w.r.t. (q, k, v).  With RoPE tables, q and k are the rotated
     tensors of the forward and dQ/dK come back in the un-rotated basis."""
+    b, hq, t, d = q.shape
+    hkv = k.shape[1]
+    dq = torch.empty((b, hq, t, d), device=q.device, dtype=q.dtype)
+    dk = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
+    dv = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
+    _launch_bwd(q, k, v, o, lse, dout, cos, sin, scale, dq, dk, dv)
+    return dq, dk, dv
+
+
+def _launch_bwd(q, k, v, o, lse, dout, cos, sin, scale, dq, dk, dv):
+    """dq/dk/dv: outputs of q/k/v's shapes, any kernel-ready strides."""
     lib = _native.load()
     q, k, v, o = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(o)
     dout = _kernel_ready(dout.to(q.dtype))
     lse = lse.contiguous()
     b, hq, t, d = q.shape
     hkv = k.shape[1]
-    dq = torch.empty((b, hq, t, d), device=q.device, dtype=q.dtype)
-    dk = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
-    dv = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
     strides = _strides(q, k, v, o, dout, dq, dk, dv)
     with torch.cuda.device(q.device):
         ws_bytes = lib.mt_gqa_attn_bwd_workspace_size(b, hq, hkv, t, d)
@@ -328,12 +376,53 @@ def gqa_attn_bwd(
             b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
         )
     _native.check(rc, "mt_gqa_attn_bwd")
-    return dq, dk, dv
 
 
 @gqa_attn_bwd.register_fake
 def _gqa_attn_bwd_fake(q, k, v, o, lse, dout, cos, sin, scale):
     return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
+
+
+@torch.library.custom_op("mega_trading_amd::gqa_rope_attn_packed_fwd", mutates_args=(), device_types="cuda")
+def gqa_rope_attn_packed_fwd(
+    qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, hq: int, hkv: int, scale: float
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns (out [B, T, Hq*D], lse, q_rot, k_rot) for a packed qkv."""
+    q, k, v = _packed_views(qkv, hq, hkv)
+    b, _, t, d = q.shape
+    out = torch.empty((b, t, hq, d), device=qkv.device, dtype=qkv.dtype)
+    _out, lse, q_rot, k_rot = _launch_fwd(q, k, v, cos, sin, scale, out=out.transpose(1, 2))
+    return out.view(b, t, hq * d), lse, q_rot, k_rot
+
+
+@gqa_rope_attn_packed_fwd.register_fake
+def _gqa_rope_attn_packed_fwd_fake(qkv, cos, sin, hq, hkv, scale):
+    b, t, width = qkv.shape
+    d = width // (hq + 2 * hkv)
+    return (qkv.new_empty((b, t, hq * d)), qkv.new_empty((b, hq, t), dtype=torch.float32),
+            qkv.new_empty((b, hq, t, d)), qkv.new_empty((b, hkv, t, d)))
+
+
+@torch.library.custom_op("mega_trading_amd::gqa_attn_bwd_packed", mutates_args=(), device_types="cuda")
+def gqa_attn_bwd_packed(
+    q_rot: torch.Tensor, k_rot: torch.Tensor, qkv: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
+    dout: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, hq: int, hkv: int, scale: float,
+) -> torch.Tensor:
+    """Gradient w.r.t. the packed qkv (un-rotated basis), in qkv's layout."""
+    _q, _k, v = _packed_views(qkv, hq, hkv)
+    b, t, _ = qkv.shape
+    d = v.shape[-1]
+    dqkv = torch.empty((b, t, qkv.shape[-1]), device=qkv.device, dtype=qkv.dtype)
+    dq, dk, dv = _packed_views(dqkv, hq, hkv)
+    o = out.view(b, t, hq, d).transpose(1, 2)
+    do = dout.reshape(b, t, hq, d).transpose(1, 2)
+    _launch_bwd(q_rot, k_rot, v, o, lse, do, cos, sin, scale, dq, dk, dv)
+    return dqkv
+
+
+@gqa_attn_bwd_packed.register_fake
+def _gqa_attn_bwd_packed_fake(q_rot, k_rot, qkv, out, lse, dout, cos, sin, hq, hkv, scale):
+    return qkv.new_empty(qkv.shape)
 
 
 @torch.library.custom_op("mega_trading_amd::gqa_attn_decode", mutates_args=(), device_types="cuda")
@@ -445,5 +534,24 @@ def _rope_fwd_backward(ctx, grad_out, _grad_lse, _grad_q_rot, _grad_k_rot):
     return dq, dk, dv, None, None, None
 
 
+def _packed_setup_context(ctx, inputs, output):
+    qkv, cos, sin, hq, hkv, scale = inputs
+    out, lse, q_rot, k_rot = output
+    ctx.save_for_backward(q_rot, k_rot, qkv, out, lse, cos, sin)
+    ctx.hq, ctx.hkv, ctx.scale = hq, hkv, scale
+    ctx.mark_non_differentiable(lse, q_rot, k_rot)
+    ctx.set_materialize_grads(False)
+
+
+def _packed_backward(ctx, grad_out, _grad_lse, _grad_q_rot, _grad_k_rot):
+    if grad_out is None:
+        return None, None, None, None, None, None
+    q_rot, k_rot, qkv, out, lse, cos, sin = ctx.saved_tensors
+    dqkv = torch.ops.mega_trading_amd.gqa_attn_bwd_packed(q_rot, k_rot, qkv, out, lse, grad_out, cos, sin, ctx.hq,
+                                                          ctx.hkv, ctx.scale)
+    return dqkv, None, None, None, None, None
+
+
 gqa_attn_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
+gqa_rope_attn_packed_fwd.register_autograd(_packed_backward, setup_context=_packed_setup_context)
 gqa_rope_attn_fwd.register_autograd(_rope_fwd_backward, setup_context=_rope_fwd_setup_context)

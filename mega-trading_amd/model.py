@@ -40,6 +40,7 @@ from .attention import attention as _hip_attention
 from .attention import decode_attention as _hip_decode_attention
 from .attention import decode_rope_append as _hip_decode_rope_append
 from .attention import rope_attention as _hip_rope_attention
+from .attention import rope_attention_packed as _hip_rope_attention_packed
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
 from .ops import add_rms_norm_mixed as _hip_add_rms_norm_mixed
 from .ops import rms_norm as _hip_rms_norm
@@ -326,8 +327,20 @@ class LlamaAttention(nn.Module):
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         batch_size, sequence_length, hidden_dim = hidden.shape
-        query, key, value = self._heads(hidden)
         dropout_p = self.dropout if self.training else 0.0
+        if self.attention_backend == "hip" and self.fuse_rope and dropout_p == 0.0:
+            # one q|k|v GEMM whose packed output the fused-RoPE kernels read in
+            # place; they write the output in the o-projection's layout and
+            # the backward writes one packed q|k|v gradient
+            qkv = _project_packed(hidden, (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
+            if qkv.dtype in (torch.bfloat16, torch.float16):
+                return self._out(_hip_rope_attention_packed(qkv, self.rope.cos, self.rope.sin,
+                                                            heads=self.attention_heads, kv_heads=self.kv_heads))
+            d = self.head_dim
+            query, key, value = self._head_views(*torch.split(
+                qkv, [self.attention_heads * d, self.kv_heads * d, self.kv_heads * d], dim=-1))
+        else:
+            query, key, value = self._heads(hidden)
         if self.attention_backend in HIP_BACKENDS and dropout_p == 0.0:
             if self.fuse_rope:
                 attended = _hip_rope_attention(query, key, value, self.rope.cos, self.rope.sin, repeats=self.repeats)
@@ -345,11 +358,12 @@ class LlamaAttention(nn.Module):
     def _heads(self, hidden: torch.Tensor):
         """[B, T, H*D] projections -> [B, H, T, D] strided views, as model.py:220-222.
         On "hip" the three products come from one GEMM (``projection.project``)."""
-        b, t, _ = hidden.shape
         if self.attention_backend == "hip":
-            query, key, value = _project(hidden, (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight))
-        else:
-            query, key, value = self.q_proj(hidden), self.k_proj(hidden), self.v_proj(hidden)
+            return self._head_views(*_project(hidden, (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)))
+        return self._head_views(self.q_proj(hidden), self.k_proj(hidden), self.v_proj(hidden))
+
+    def _head_views(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor):
+        b, t, _ = query.shape
         query = query.view(b, t, self.attention_heads, self.head_dim).transpose(1, 2)
         key = key.view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)
         value = value.view(b, t, self.kv_heads, self.head_dim).transpose(1, 2)

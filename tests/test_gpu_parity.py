@@ -154,6 +154,32 @@ def test_model_layout_views_and_strided_grad(mta):
     assert max(rel(f(qd.grad), edq1), rel(f(kd.grad), edk1), rel(f(vd.grad), edv1)) <= TOL_GRAD_REL
 
 
+@pytest.mark.parametrize("b,t,hq,hkv,d,dt", [(2, 1024, 8, 2, 64, torch.bfloat16), (1, 333, 4, 4, 128, torch.float16),
+                                            (3, 200, 6, 2, 32, torch.bfloat16)])
+def test_packed_qkv_equals_the_head_views(mta, b, t, hq, hkv, d, dt):
+    """rope_attention_packed on one [B, T, (Hq + 2 Hkv) D] projection output: the
+    same kernels with other strides, so output and packed gradient equal
+    rope_attention on the three head views bit for bit."""
+    from importlib import import_module
+    attn = import_module("mega-trading_amd.attention")
+    model_mod = import_module("mega-trading_amd.model")
+    g = torch.Generator().manual_seed(t + d)
+    qkv = (torch.randn(b, t, (hq + 2 * hkv) * d, generator=g) * 0.5).to(dt).cuda()
+    dout = torch.randn(b, t, hq * d, generator=g).to(dt).cuda()
+    rope = model_mod.RotaryEmbedding(d, 1024, theta=10_000.0).cuda()
+    a = qkv.clone().requires_grad_(True)
+    out = attn.rope_attention_packed(a, rope.cos, rope.sin, heads=hq, kv_heads=hkv)
+    out.backward(dout)
+    q, k, v = (x.detach().clone().requires_grad_(True) for x in attn._packed_views(qkv, hq, hkv))
+    ref = attn.rope_attention(q, k, v, rope.cos, rope.sin, repeats=hq // hkv)
+    ref.backward(dout.view(b, t, hq, d).transpose(1, 2))
+    torch.cuda.synchronize()
+    assert out.shape == (b, t, hq * d) and out.is_contiguous()
+    assert torch.equal(out, ref.transpose(1, 2).reshape(b, t, hq * d))
+    dq, dk, dv = attn._packed_views(a.grad, hq, hkv)
+    assert torch.equal(dq, q.grad) and torch.equal(dk, k.grad) and torch.equal(dv, v.grad)
+
+
 def test_causality_and_determinism_at_full_size(mta):
     """C3 shape: changing keys/values at positions >= t0 leaves output rows < t0
     bit-identical, and repeated runs are bit-identical (no atomics anywhere)."""
