@@ -42,6 +42,7 @@ from .attention import decode_rope_append as _hip_decode_rope_append
 from .attention import rope_attention as _hip_rope_attention
 from .attention import rope_attention_packed as _hip_rope_attention_packed
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
+from .ops import add_rms_norm as _hip_add_rms_norm
 from .ops import add_rms_norm_mixed as _hip_add_rms_norm_mixed
 from .ops import rms_norm as _hip_rms_norm
 from .ops import rms_norm_mixed as _hip_rms_norm_mixed
@@ -197,28 +198,60 @@ class TradingModel(nn.Module):
         """Forward over the prompt that also fills per-layer KV caches of capacity
         block_size: the caches given in ``into`` when their shape and dtype fit
         (then ``reused`` is True), else new ones.  Returns (logits, caches, reused)."""
-        hidden = self.token_embedding(tokens)
         cache = []
         reused = into is not None
-        for i, block in enumerate(self.blocks):
-            attended, k_cache, v_cache = block.attention.prefill(
-                block.attention_norm(hidden), self.block_size, into[i] if into is not None else None)
+
+        def attend(i, block, normed):
+            nonlocal reused
+            attended, k_cache, v_cache = block.attention.prefill(normed, self.block_size,
+                                                                 into[i] if into is not None else None)
             reused = reused and k_cache is into[i][0]
             cache.append((k_cache, v_cache))
-            hidden = hidden + attended
-            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
-        return self.output(self.norm(hidden))[:, -1, :], cache, reused
+            return attended
+
+        normed = self._residual_chain(self.token_embedding(tokens), attend)
+        return self.output(normed)[:, -1, :], cache, reused
 
     def _decode(self, token: torch.Tensor, cache, pos) -> torch.Tensor:
         """Logits after the token at position ``pos`` (its K/V are appended to the
         caches).  ``pos`` is an int, or a one-element int32 GPU tensor that the
         kernels read when they run (the form a recorded HIP graph replays)."""
         length = pos + 1
-        hidden = self.token_embedding(token)
-        for block, (k_cache, v_cache) in zip(self.blocks, cache):
-            hidden = hidden + block.attention.decode(block.attention_norm(hidden), k_cache, v_cache, pos, length)
-            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
-        return self.output(self.norm(hidden))[:, -1, :]
+
+        def attend(i, block, normed):
+            k_cache, v_cache = cache[i]
+            return block.attention.decode(normed, k_cache, v_cache, pos, length)
+
+        return self.output(self._residual_chain(self.token_embedding(token), attend))[:, -1, :]
+
+    def _residual_chain(self, hidden: torch.Tensor, attend) -> torch.Tensor:
+        """The blocks (``model.py:184-187`` each) and the final norm over the
+        residual stream ``hidden``, with ``attend(i, block, normed)`` for the
+        attention call (training, prefill and decode differ only there);
+        returns the final norm's output.  With the norms on HIP ("hip") every residual add is fused
+        into the norm that reads its sum (the block's FFN norm, the next
+        block's attention norm, or the final norm): ``ops.add_rms_norm`` when
+        the branch and the stream share a dtype, ``ops.add_rms_norm_mixed``
+        for a 16-bit branch on an fp32 stream under autocast, whose norms then
+        write the autocast dtype that the next projection would cast to.
+        Both are bit-identical to the add followed by the norm (and the cast)."""
+        if self.norm.operator_backend != "hip":
+            for i, block in enumerate(self.blocks):
+                hidden = hidden + attend(i, block, block.attention_norm(hidden))
+                hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
+            return self.norm(hidden)
+        act = None
+        if (hidden.is_cuda and hidden.dtype == torch.float32 and torch.is_autocast_enabled("cuda")
+                and torch.get_autocast_dtype("cuda") in (torch.bfloat16, torch.float16)
+                and self.norm.weight.dtype == torch.float32):
+            act = torch.get_autocast_dtype("cuda")
+        first = self.blocks[0].attention_norm if len(self.blocks) else self.norm
+        normed = _hip_rms_norm_mixed(hidden, first.weight, eps=first.eps, out_dtype=act) if act else first(hidden)
+        for i, block in enumerate(self.blocks):
+            nxt = self.blocks[i + 1].attention_norm if i + 1 < len(self.blocks) else self.norm
+            hidden, normed = _add_norm(attend(i, block, normed), hidden, block.ffn_norm)
+            hidden, normed = _add_norm(block.feed_forward(normed), hidden, nxt)
+        return normed
 
     def _hidden(self, input_ids: torch.Tensor) -> torch.Tensor:
         if input_ids.ndim != 2:
@@ -226,34 +259,11 @@ class TradingModel(nn.Module):
         if input_ids.shape[1] > self.block_size:
             raise ValueError(f"sequence length {input_ids.shape[1]} exceeds block_size {self.block_size}")
         hidden = self.token_embedding(input_ids)
-        if self._fused_norms(hidden):
-            return self._hidden_fused(hidden)
+        if self.norm.operator_backend == "hip":
+            return self._residual_chain(hidden, lambda i, block, normed: block.attention(normed))
         for block in self.blocks:
             hidden = block(hidden)
         return self.norm(hidden)
-
-    def _fused_norms(self, hidden: torch.Tensor) -> bool:
-        """The "hip" route under 16-bit CUDA autocast with an fp32 residual stream."""
-        return (self.operator_backend == "hip" and hidden.is_cuda and hidden.dtype == torch.float32
-                and torch.is_autocast_enabled("cuda")
-                and torch.get_autocast_dtype("cuda") in (torch.bfloat16, torch.float16)
-                and self.norm.weight.dtype == torch.float32)
-
-    def _hidden_fused(self, hidden: torch.Tensor) -> torch.Tensor:
-        """The blocks of ``_hidden`` (``model.py:184-187`` each) with every
-        residual add fused into the RMSNorm that reads its sum: the next
-        block's attention norm, the block's FFN norm, or the final norm.  The
-        norms write the autocast dtype that the following projection would
-        cast to; the residual stream stays fp32 (``ops.add_rms_norm_mixed``)."""
-        act = torch.get_autocast_dtype("cuda")
-        first = self.blocks[0].attention_norm if len(self.blocks) else self.norm
-        normed = _hip_rms_norm_mixed(hidden, first.weight, eps=first.eps, out_dtype=act)
-        for i, block in enumerate(self.blocks):
-            nxt = self.blocks[i + 1].attention_norm if i + 1 < len(self.blocks) else self.norm
-            ffn_norm = block.ffn_norm
-            hidden, normed = _hip_add_rms_norm_mixed(block.attention(normed), hidden, ffn_norm.weight, eps=ffn_norm.eps)
-            hidden, normed = _hip_add_rms_norm_mixed(block.feed_forward(normed), hidden, nxt.weight, eps=nxt.eps)
-        return normed
 
 
 class LlamaDecoderBlock(nn.Module):
@@ -510,6 +520,17 @@ class _DecodeGraph:
                 self.out = self.model._decode(self.tok, self.cache, self.pos)
         self.graph.replay()
         return self.out
+
+
+def _add_norm(branch: torch.Tensor, hidden: torch.Tensor, norm: "RMSNorm") -> tuple[torch.Tensor, torch.Tensor]:
+    """(hidden + branch, norm(hidden + branch)) with the add fused into the HIP norm."""
+    if branch.dtype == hidden.dtype:
+        return _hip_add_rms_norm(branch, hidden, norm.weight, eps=norm.eps)
+    if (hidden.dtype == torch.float32 and branch.dtype in (torch.bfloat16, torch.float16)
+            and norm.weight.dtype == torch.float32):
+        return _hip_add_rms_norm_mixed(branch, hidden, norm.weight, eps=norm.eps)
+    hidden = hidden + branch
+    return hidden, norm(hidden)
 
 
 def _sample_next(logits: torch.Tensor, top_k: int) -> torch.Tensor:

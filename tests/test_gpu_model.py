@@ -68,3 +68,33 @@ def test_c5_full_shape_step_runs_through_hip_kernels():
     assert abs(loss - math.log(16384)) < 0.5, loss
     loss2 = float(step())
     assert math.isfinite(loss2) and loss2 < loss
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_fused_residual_chain_equals_the_block_loop(autocast):
+    # the "hip" model fuses each residual add into the next norm; the values
+    # equal model.py:184-187's block loop bit for bit (same fp32 adds, same
+    # norm kernel, one rounding to the autocast dtype), the gradients to rounding
+    ids, _ = workload.zipf_batch(2, 256, SMALL["vocab_size"], seed=3)
+    ids = ids.cuda()
+    m = workload.build_model("hip", seed=0, device="cuda", **SMALL)
+    params = [p for p in m.parameters()]
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16, enabled=autocast):
+        fused = m._hidden(ids)
+        h = m.token_embedding(ids)
+        for block in m.blocks:
+            h = block(h)
+        ref = m.norm(h)
+    assert fused.dtype == (torch.bfloat16 if autocast else torch.float32)
+    assert torch.equal(fused, ref.to(fused.dtype))
+    g = torch.randn(fused.shape, generator=torch.Generator().manual_seed(4)).cuda()
+    ga = torch.autograd.grad((fused.float() * g).sum(), params, allow_unused=True)
+    gb = torch.autograd.grad((ref.to(fused.dtype).float() * g).sum(), params, allow_unused=True)
+    for a, b in zip(ga, gb):
+        if a is None or b is None:
+            assert a is None and b is None
+            continue
+        # the fused backward adds the residual gradient inside the norm kernel
+        # (possibly contracted into an fma): last-ulp fp32 differences that can
+        # flip bf16 roundings in the attention backward, which runs in bf16
+        assert _rel(a.float(), b.float()) <= 1e-3
