@@ -35,6 +35,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import importlib
 import json
 import math
@@ -415,10 +416,15 @@ def generate_tokens_per_second(pkg, rollouts=32, prompt=512, new_tokens=64):
         # set-up stay out of the timed call, for both routes alike
         model.generate(ids, max_new_tokens=new_tokens)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        model.generate(ids, max_new_tokens=new_tokens)
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
+        gc.collect()
+        gc.freeze()  # as TrainStep.tokens_per_second: no full collection inside the timed call
+        try:
+            t0 = time.perf_counter()
+            model.generate(ids, max_new_tokens=new_tokens)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+        finally:
+            gc.unfreeze()
         out[name] = {"tokens_per_s": round(rollouts * new_tokens / dt, 1), "ms_per_token": round(dt / new_tokens * 1e3, 3)}
         del model
         torch.cuda.empty_cache()

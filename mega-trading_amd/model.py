@@ -160,12 +160,12 @@ class TradingModel(nn.Module):
             return self._generate_recompute(input_ids, max_new_tokens, top_k)
         tokens = input_ids
         cache = step = None
-        key = (tokens.shape[0], tokens.device)
+        key = (tokens.shape[0], tokens.device, top_k)
         for _ in range(max_new_tokens):
             t = tokens.shape[1]
             if t > self.block_size:
                 cache = step = None
-                logits = self(tokens[:, -self.block_size:])[:, -1, :]
+                nxt = _sample_next(self(tokens[:, -self.block_size:])[:, -1, :], top_k)
             elif cache is None:
                 # prefill into the kept caches when a recording for this batch exists
                 state = self._gen_state if self.decode_graphs else None
@@ -174,14 +174,15 @@ class TradingModel(nn.Module):
                 step = state[2] if reuse and reused else None
                 if reuse and not reused:
                     self._gen_state = None
+                nxt = _sample_next(logits, top_k)
             elif self.decode_graphs:
                 if step is None:
-                    step = _DecodeGraph(self, cache, tokens.shape[0], tokens.device)
+                    step = _DecodeGraph(self, cache, tokens.shape[0], tokens.device, top_k=top_k)
                     self._gen_state = (key, cache, step)
-                logits = step(tokens[:, -1:], t - 1)
+                nxt = step(tokens[:, -1:], t - 1)  # the recorded step samples too
             else:
-                logits = self._decode(tokens[:, -1:], cache, t - 1)
-            tokens = torch.cat([tokens, _sample_next(logits, top_k)], dim=1)
+                nxt = _sample_next(self._decode(tokens[:, -1:], cache, t - 1), top_k)
+            tokens = torch.cat([tokens, nxt], dim=1)
         return tokens
 
     @torch.no_grad()
@@ -495,12 +496,15 @@ class _DecodeGraph:
     every position; the host only writes the next token and position before
     each replay.  Replaying a step again for the same position rewrites the
     same cache row with the same values, so the first call (warm-up, record,
-    replay) is harmless.  The returned logits are the graph's static buffer,
-    valid until the next call."""
+    replay) is harmless.  The result is the graph's static buffer, valid until
+    the next call: the logits, or with ``top_k`` set the sampled next tokens
+    [batch, 1] (``_sample_recorded``: the reference's top-k multinomial draw
+    without its host-side validity check, so the sampling is recorded too)."""
 
-    def __init__(self, model: "TradingModel", cache, batch: int, device: torch.device):
+    def __init__(self, model: "TradingModel", cache, batch: int, device: torch.device, top_k=None):
         self.model = model
         self.cache = cache
+        self.top_k = top_k
         self.tok = torch.zeros((batch, 1), dtype=torch.long, device=device)
         self.pos = torch.zeros((1,), dtype=torch.int32, device=device)
         self.graph = None
@@ -518,6 +522,8 @@ class _DecodeGraph:
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph):
                 self.out = self.model._decode(self.tok, self.cache, self.pos)
+                if self.top_k is not None:
+                    self.out = _sample_recorded(self.out, self.top_k)
         self.graph.replay()
         return self.out
 
@@ -540,6 +546,19 @@ def _sample_next(logits: torch.Tensor, top_k: int) -> torch.Tensor:
         logits = logits.masked_fill(logits < values[:, [-1]], float("-inf"))
     probs = torch.softmax(logits, dim=-1)
     return torch.multinomial(probs, num_samples=1)
+
+
+def _sample_recorded(logits: torch.Tensor, top_k: int) -> torch.Tensor:
+    """``_sample_next`` in a form a HIP graph can record.  For one sample
+    ``torch.multinomial`` draws argmax(p / E) with E ~ Exponential(1) from the
+    same generator, after a host-synchronising check that p holds no inf, NaN
+    or negative value; this is that draw without the check (same tokens for
+    the same generator state)."""
+    if top_k > 0:
+        values, _ = torch.topk(logits, min(top_k, logits.shape[-1]))
+        logits = logits.masked_fill(logits < values[:, -1:], float("-inf"))  # a slice: no host index tensor
+    probs = torch.softmax(logits, dim=-1)
+    return torch.argmax(probs / torch.empty_like(probs).exponential_(1), dim=-1, keepdim=True)
 
 
 def rotate(value: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:

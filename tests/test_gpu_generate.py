@@ -197,3 +197,28 @@ def test_generate_reuses_the_recorded_step_across_calls():
     third = m.generate(p3, max_new_tokens=8, top_k=1)
     assert m._gen_state is not state and m._gen_state[0][0] == 5
     assert torch.equal(third, fresh.generate(p3, max_new_tokens=8, top_k=1))
+
+
+def test_recorded_sampling_reproduces_the_eager_draw():
+    # the recorded step samples with torch.multinomial's one-sample draw minus
+    # its host-synchronising check: the same tokens for the same seed, for the
+    # draw alone and for whole top-k 16 generations (recording call and reuse)
+    g = torch.Generator().manual_seed(35)
+    logits = (torch.randn(6, 128, generator=g) * 3).cuda()
+    for k in (1, 16, 0):
+        torch.manual_seed(9)
+        x = model_mod._sample_next(logits, k)
+        torch.manual_seed(9)
+        y = model_mod._sample_recorded(logits, k)
+        assert torch.equal(x, y), k
+    m = _model("hip", block_size=64)
+    prompt = torch.randint(0, 128, (3, 10), generator=g).cuda()
+    torch.manual_seed(5)
+    m.decode_graphs = False
+    eager = m.generate(prompt, max_new_tokens=20, top_k=16)
+    m.decode_graphs = True
+    torch.manual_seed(5)
+    recorded = m.generate(prompt, max_new_tokens=20, top_k=16)
+    torch.manual_seed(5)
+    reused = m.generate(prompt, max_new_tokens=20, top_k=16)
+    assert torch.equal(eager, recorded) and torch.equal(recorded, reused)
