@@ -26,6 +26,7 @@ from typing import Optional
 import torch
 
 from . import _native
+from .gemm_tuning import tuned_gemms
 
 __all__ = ["rms_norm", "add_rms_norm", "rms_norm_mixed", "add_rms_norm_mixed", "swiglu_gate", "swiglu_gate_packed",
            "fused_linear_cross_entropy", "MAX_NORM_DIM"]
@@ -492,7 +493,7 @@ def fused_linear_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Te
         gh = torch.empty((rows, h), device=hidden.device, dtype=ct)
         gw = torch.zeros((vocab, h), device=hidden.device, dtype=torch.float32)
     chunk = max(1, min(rows, _CE_CHUNK_BYTES // (vocab * ct.itemsize)))
-    with torch.cuda.device(hidden.device):
+    with torch.cuda.device(hidden.device), tuned_gemms():
         stream = _stream(hidden)
         for start in range(0, rows, chunk):
             end = min(rows, start + chunk)

@@ -28,6 +28,8 @@ from typing import Sequence
 
 import torch
 
+from .gemm_tuning import tuned_gemms
+
 __all__ = ["project", "project_packed", "split_k_chunks"]
 
 _MIN_CHUNK_ROWS = 1024
@@ -78,7 +80,8 @@ class _Project(torch.autograd.Function):
         with torch.autocast("cuda", enabled=False):
             w = weights[0].to(dtype) if len(weights) == 1 else torch.cat([v.to(dtype) for v in weights])
             x2 = x.reshape(-1, x.shape[-1]).to(dtype)
-            y = x2 @ w.t()
+            with tuned_gemms():
+                y = x2 @ w.t()
         ctx.save_for_backward(x2, w)
         ctx.outs = [v.shape[0] for v in weights]
         ctx.x_shape = x.shape
@@ -89,7 +92,10 @@ class _Project(torch.autograd.Function):
     def backward(ctx, dy):
         x2, w = ctx.saved_tensors
         dy = dy.reshape(x2.shape[0], w.shape[0]).to(w.dtype)
-        dx = (dy @ w).view(ctx.x_shape) if ctx.needs_input_grad[0] else None
+        dx = None
+        if ctx.needs_input_grad[0]:
+            with tuned_gemms():
+                dx = (dy @ w).view(ctx.x_shape)
         dws = [None] * len(ctx.outs)
         if any(ctx.needs_input_grad[2:]):
             dw = _weight_grad(dy, x2)

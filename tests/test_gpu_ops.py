@@ -385,3 +385,22 @@ def test_cross_entropy_rows_streaming_vocab(mta):
     assert abs(loss.item() - rl) <= 1e-4 * abs(rl)
     assert _rel(hg.grad.cpu().numpy(), rgh) < 1e-4
     assert _rel(wg.grad.cpu().numpy(), rgw) < 1e-4
+
+
+def test_tuned_gemm_replay_is_scoped_and_the_results_file_applies():
+    # the committed results match this runtime (else TunableOp ignores them) and
+    # the replay is switched on only inside tuned_gemms(), with tuning off,
+    # leaving the process-wide TunableOp state as it was
+    from importlib import import_module
+    gt = import_module("mega-trading_amd.gemm_tuning")
+    tun = torch.cuda.tunable
+    assert gt._load(), "tuned/gemm_gfx950.csv does not validate against this runtime"
+    before = (tun.is_enabled(), tun.tuning_is_enabled())
+    with gt.tuned_gemms():
+        assert tun.is_enabled() and not tun.tuning_is_enabled()
+        a = torch.randn(32768, 512, device="cuda").bfloat16()
+        w = torch.randn(768, 512, device="cuda").bfloat16()
+        y = a @ w.t()
+    assert (tun.is_enabled(), tun.tuning_is_enabled()) == before
+    ref = a.double() @ w.double().t()
+    assert ((y.double() - ref).norm() / ref.norm()).item() < 2 ** -8

@@ -255,3 +255,12 @@ def test_hip_route_projections_match_the_linear_modules():
                                [g.transpose(1, 2).reshape(2, 16, -1) for g in gs[:3]] + [gs[3]])
     for a, b in zip(got, want):
         torch.testing.assert_close(a, b)
+
+
+def test_tuned_gemm_context_is_inert_without_a_gpu():
+    gt = importlib.import_module("mega-trading_amd.gemm_tuning")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with gt.tuned_gemms():
+        x = torch.randn(4, 8) @ torch.randn(8, 3)
+    assert x.shape == (4, 3) and gt._load() is False
