@@ -685,10 +685,31 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
 // The two 32-key halves mt run one after the other and each K / V operand
 // read from LDS (row reads for S^T / dP^T, transposed reads for dQ) feeds
 // both 32-query halves nt of the wave.
+// Per-wave LDS block of the dQ softmax offsets, each query's value stored 16
+// times: [kind: 0 = -LSE log2(e), 1 = -delta][32-query half nt][group g][query
+// l32][4 copies].  A lane's 16 accumulator slots all belong to its query, so
+// four ds_read_b128 (one per group, 16 consecutive lanes reading 256
+// consecutive bytes) give the MFMA accumulator its starting value without VALU
+// work; the score MFMA then yields S c2 - LSE2 (Q pre-scaled by c2) and the dP
+// MFMA yields dP - delta.
+constexpr int kDqOffsFloats = 2 * 2 * 4 * 32 * 4;  // per wave (8 KB)
+
+__device__ __forceinline__ f32x16 dq_offset_tile(const float* offs, int kind, int nt, int l32) {
+  const float* b = offs + (kind * 2 + nt) * 512 + l32 * 4;
+  f32x16 r;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(b + g * 128);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[4 * g + c] = v[c];
+  }
+  return r;
+}
+
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typename E::v8 (*qop)[D / 16],
-                                        const typename E::v8 (*gop)[D / 16], f32x16 (*dqacc)[2], const float* lse2,
-                                        const float* dlt, int rbase, TrBase tbase, int l32, int hh, float c2) {
+                                        const typename E::v8 (*gop)[D / 16], f32x16 (*dqacc)[2], const float* offs,
+                                        int rbase, TrBase tbase, int l32, int hh) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
@@ -701,8 +722,9 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
       const V8 b = TL::template row_op<E>(Vr, rbase, mt * 32, 0);
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        st[nt] = E::mfma(a, qop[nt][0], f32x16{});
-        dpt[nt] = E::mfma(b, gop[nt][0], f32x16{});
+        // accumulators start at -LSE log2(e) and -delta of the lane's query
+        st[nt] = E::mfma(a, qop[nt][0], dq_offset_tile(offs, 0, nt, l32));
+        dpt[nt] = E::mfma(b, gop[nt][0], dq_offset_tile(offs, 1, nt, l32));
       }
     }
 #pragma unroll
@@ -720,12 +742,12 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
     for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float pv = exp2_fast(__builtin_fmaf(st[nt][i], c2, -lse2[nt]));
+        float pv = exp2_fast(st[nt][i]);
         if constexpr (MASK) {
           const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
           if (kr > nt * 32 + l32) pv = 0.f;
         }
-        st[nt][i] = pv * (dpt[nt][i] - dlt[nt]);
+        st[nt][i] = pv * dpt[nt][i];
       }
       dsb[nt][0] = pack8<E>(st[nt], 0);
       dsb[nt][1] = pack8<E>(st[nt], 8);
@@ -756,6 +778,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
   __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
+  __shared__ __attribute__((aligned(16))) float offs_all[4][kDqOffsFloats];
 
   const RowTask task = row_task(p);
   const int tid = threadIdx.x;
@@ -768,13 +791,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
   const int q0 = qb * kBlk;
   const bool active = qb < p.nqb;
   const int jlast = min(p.nqb - 1, task.sb * p.rb + p.rb - 1);
+  float* offs = offs_all[wave];
 
   const uint16_t* kbase = p.k + task.b * p.sk[0] + (int64_t)task.kvh * p.sk[1];
   const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
   const int64_t rowbase = ((int64_t)task.b * p.Hq + head) * p.T;
 
   V8 qop[2][KT], gop[2][KT];
-  float lse2[2], dlt[2];
   {
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     const uint16_t* gbase = p.dout + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
@@ -795,6 +818,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
       }
       lx[nt] = p.lse[rowbase + rc];
     }
+    const float c2 = p.scale_log2;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int row = q0 + nt * 32 + l32;
@@ -802,7 +826,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
       float dsum = 0.f;
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
-        qop[nt][kk] = __builtin_bit_cast(V8, ok ? qx[nt][kk] : zero4());
+        // Q pre-multiplied by scale * log2(e) (rounded to the storage type once,
+        // as the dK/dV pass does with K), so the score MFMA yields S c2 directly
+        u32x4 qs = ok ? qx[nt][kk] : zero4();
+#pragma unroll
+        for (int w = 0; w < 4; ++w) qs[w] = pack2<E>(lo_f<E>(qs[w]) * c2, hi_f<E>(qs[w]) * c2);
+        qop[nt][kk] = __builtin_bit_cast(V8, qs);
         const u32x4 g = ok ? gx[nt][kk] : zero4();
         const u32x4 o = ox[nt][kk];
         gop[nt][kk] = __builtin_bit_cast(V8, g);
@@ -811,11 +840,17 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
           dsum += lo_f<E>(g[w]) * lo_f<E>(o[w]) + hi_f<E>(g[w]) * hi_f<E>(o[w]);
       }
       dsum = sum_with_partner(dsum);
-      dlt[nt] = dsum;
-      lse2[nt] = ok ? lx[nt] * kLog2e : 0.f;
+      const float lse2 = ok ? lx[nt] * kLog2e : 0.f;
       if (ok && hh == 0) {  // negated: the dK/dV pass seeds its accumulators with them
         p.ndelta[rowbase + row] = -dsum;
-        p.nlse2[rowbase + row] = -lse2[nt];
+        p.nlse2[rowbase + row] = -lse2;
+      }
+      // this wave's offset block: lanes hh = 0 / 1 fill groups 0-1 / 2-3
+      const f32x4 nl = {-lse2, -lse2, -lse2, -lse2}, nd = {-dsum, -dsum, -dsum, -dsum};
+#pragma unroll
+      for (int g = 2 * hh; g < 2 * hh + 2; ++g) {
+        *reinterpret_cast<f32x4*>(offs + (0 * 2 + nt) * 512 + g * 128 + l32 * 4) = nl;
+        *reinterpret_cast<f32x4*>(offs + (1 * 2 + nt) * 512 + g * 128 + l32 * 4) = nd;
       }
     }
   }
@@ -837,7 +872,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
   wait_vmem();
   __syncthreads();
 
-  const float c2 = p.scale_log2;
   for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
     const int buf = j & 1;
     if (j < jlast) {
@@ -846,16 +880,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
     }
     if (active && j <= qb) {
       if (PEEL || j < qb)
-        dq_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh, c2);
+        dq_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
       else
-        dq_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh, c2);
+        dq_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
     }
     wait_vmem();
     __syncthreads();
   }
   if (PEEL && active)  // qb == jlast
-    dq_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32,
-                        hh, c2);
+    dq_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
 
   if (!active) return;
   uint16_t* dqbase = p.out + task.b * p.sout[0] + (int64_t)head * p.sout[1];
