@@ -106,3 +106,24 @@ class TrainStep:
         finally:
             gc.unfreeze()
         return self.labels.numel() * steps / elapsed, elapsed / steps * 1e3, float(loss)
+
+
+def main(argv=None) -> int:
+    """``python -m mega-trading_amd.workload [--route hip] [--steps 5] [--warmup 3]``:
+    the BASELINE config 5 train step on one route, tokens/sec on one line."""
+    import argparse
+
+    ap = argparse.ArgumentParser(description=main.__doc__)
+    ap.add_argument("--route", default="hip", help='attention backend: "hip", "triton" or "auto" (SDPA)')
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=3)
+    args = ap.parse_args(argv)
+    ids, labels = zipf_batch(C5_BATCH, C5_SEQ, C5_MODEL["vocab_size"])
+    step = TrainStep(build_model(args.route, seed=0, device="cuda"), ids, labels)
+    tps, ms, loss = step.tokens_per_second(args.steps, args.warmup)
+    print(f"C5 train step, route {args.route}: {tps:.0f} tokens/s, {ms:.3f} ms/step, loss {loss:.4f}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
