@@ -53,7 +53,12 @@ def _load() -> bool:
 
 @contextlib.contextmanager
 def tuned_gemms():
-    """Replay the recorded GEMM solutions inside the block (no tuning)."""
+    """Replay the recorded GEMM solutions inside the block (no tuning).
+
+    The TunableOp switches are process-wide: a GEMM that another thread runs
+    while a block is open may also replay a recorded solution, and one
+    started as a block closes may not.  Either way only the choice of library
+    kernel changes, never what is computed."""
     if not (_state["tuning"] or _load()):
         yield
         return

@@ -85,6 +85,21 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     assert lib.mt_cross_entropy_rows(p, 16, p, -1, 16, p, -100, p, 1, BF16, None) == -2
     assert lib.mt_cross_entropy_rows(None, 16, None, 0, 16, None, -100, None, 1, BF16, None) == 0
     assert lib.mt_last_error() == b""
+    # packed SwiGLU: cols a multiple of 8, 16-byte pointers, rows * cols / 8 < 2^31
+    assert lib.mt_swiglu_packed_fwd(p, p, 4, 12, BF16, None) == -2
+    assert lib.mt_swiglu_packed_fwd(p, p, 1 << 30, 1 << 10, BF16, None) == -2
+    assert lib.mt_swiglu_packed_fwd(p + 8, p, 4, 16, BF16, None) == -3
+    assert lib.mt_swiglu_packed_bwd(p, None, p, 4, 16, BF16, None) == -1
+    assert lib.mt_swiglu_packed_fwd(None, None, 0, 16, BF16, None) == 0
+    # mixed norms: 16-bit activations, fp32 weight; the same shape checks as the plain norms
+    FP16 = mta._native.DTYPE_FP16
+    assert lib.mt_rms_norm_fwd_mixed(p, 16, p, p, p, 4, 16, 1e-5, FP32, FP32, None) == -4  # y must be 16-bit
+    assert lib.mt_rms_norm_fwd_mixed(p, 16, p, p, p, 4, 16, 1e-5, BF16, BF16, None) == -4  # weight must be fp32
+    assert lib.mt_rms_norm_fwd_mixed(p, 16, p, p, p, 4, 12, 1e-5, BF16, FP32, None) == -2
+    assert lib.mt_add_rms_norm_fwd_mixed(p, 16, p, 8, p, p, p, p, 4, 16, 1e-5, FP16, FP32, None) == -3
+    assert lib.mt_rms_norm_bwd_mixed(p, p, p, None, p, p, None, p, p, need - 1, 1000, 512, BF16, FP32, None) == -6
+    assert lib.mt_rms_norm_bwd_mixed(p, p, p, p + 4, p, p, None, p, p, need, 1000, 512, BF16, FP32, None) == -3
+    assert lib.mt_rms_norm_fwd_mixed(p, 16, p, p, p, 0, 16, 1e-5, BF16, FP32, None) == 0
 
 
 def test_ops_reject_cpu_tensors(mta):
@@ -200,6 +215,11 @@ def test_fake_impls_give_shapes_for_tracing(mta):
         assert out2.shape == q.shape and qr.shape == q.shape and kr.shape == k.shape
         dq, dk, dv = torch.ops.mega_trading_amd.gqa_attn_bwd(q, k, k, out, lse, q, None, None, 0.125)
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+        qkv = _fake((2, 100, (8 + 2 + 2) * 64))
+        o3, l3, qr3, kr3 = torch.ops.mega_trading_amd.gqa_rope_attn_packed_fwd(qkv, cs, cs, 8, 2, 0.125)
+        assert o3.shape == (2, 100, 512) and l3.shape == (2, 8, 100) and qr3.shape == q.shape and kr3.shape == k.shape
+        d3 = torch.ops.mega_trading_amd.gqa_attn_bwd_packed(qr3, kr3, qkv, o3, l3, o3, cs, cs, 8, 2, 0.125)
+        assert d3.shape == qkv.shape
 
 
 def test_kernel_ready_keeps_model_layout_views():
