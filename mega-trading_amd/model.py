@@ -211,7 +211,8 @@ class TradingModel(nn.Module):
             return attended
 
         normed = self._residual_chain(self.token_embedding(tokens), attend)
-        return self.output(normed)[:, -1, :], cache, reused
+        # the loss head on the last position only: the logits generate samples from
+        return self.output(normed[:, -1, :]), cache, reused
 
     def _decode(self, token: torch.Tensor, cache, pos) -> torch.Tensor:
         """Logits after the token at position ``pos`` (its K/V are appended to the
