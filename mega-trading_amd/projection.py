@@ -78,7 +78,8 @@ class _Project(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dtype, *weights):
         with torch.autocast("cuda", enabled=False):
-            w = weights[0].to(dtype) if len(weights) == 1 else torch.cat([v.to(dtype) for v in weights])
+            # one concatenation, then one cast (the same values as casting each weight)
+            w = (weights[0] if len(weights) == 1 else torch.cat(weights)).to(dtype)
             x2 = x.reshape(-1, x.shape[-1]).to(dtype)
             with tuned_gemms():
                 y = x2 @ w.t()
