@@ -56,6 +56,27 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
   if (k0 >= L) return;  // a split past the current length (device-length launches cover the capacity)
   const int n = min(kDecSplit, L - k0);
 
+  // Every K and V load of this thread is issued first, so the score, softmax
+  // and V passes wait on one memory round trip: the K row of key k0 + tid,
+  // and the 16-byte V chunks of the V pass (chunk c = tid % NC of keys
+  // tid / NC, tid / NC + G, ...).
+  constexpr int NC = D / 8;      // 16-byte chunks per V row
+  constexpr int G = 256 / NC;    // key groups of the V pass
+  constexpr int NV = kDecSplit / G;  // V chunks per thread
+  u32x4 kw[D / 8], vw[NV];
+  if (tid < n) {
+    const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + tid) * p.sk[2];
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) kw[c] = *reinterpret_cast<const u32x4*>(krow + 8 * c);
+  }
+  const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2];
+  const int c = tid % NC;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = tid / NC + i * G;
+    if (j < n) vw[i] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)j * p.sv[2] + 8 * c);
+  }
+
   for (int i = tid; i < R * D; i += 256) {
     const int h = i / D, d = i % D;
     qs[h][d] = E::to_f(p.q[b * p.sq[0] + (int64_t)(kvh * R + h) * p.sq[1] + d]);
@@ -67,10 +88,9 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
 #pragma unroll
   for (int h = 0; h < kDecMaxR; ++h) sc[h] = 0.f;
   if (tid < n) {
-    const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + tid) * p.sk[2];
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(krow + 8 * c);
+    for (int c8 = 0; c8 < D / 8; ++c8) {
+      const u32x4 w = kw[c8];
       float kv[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -81,7 +101,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
       for (int h = 0; h < kDecMaxR; ++h)
         if (h < R)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sc[h] = __builtin_fmaf(qs[h][8 * c + e], kv[e], sc[h]);
+          for (int e = 0; e < 8; ++e) sc[h] = __builtin_fmaf(qs[h][8 * c8 + e], kv[e], sc[h]);
     }
   }
   // per-head max over the split
@@ -114,21 +134,19 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) 
   __syncthreads();
 
   // o[h][d] = sum_j p[h][j] V[k0 + j][d].  Thread t takes the 8-value d chunk
-  // c = t % NC of keys j = t / NC, t / NC + G, ... (one 16-byte load per key
-  // feeds 8 d values of every head), then the G key groups are summed
-  // through LDS.
-  constexpr int NC = D / 8;      // 16-byte chunks per V row
-  constexpr int G = 256 / NC;    // key groups
-  const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2];
-  const int c = tid % NC;
+  // c = t % NC of keys j = t / NC, t / NC + G, ... (one 16-byte load per key,
+  // issued at the start, feeds 8 d values of every head), then the G key
+  // groups are summed through LDS.
   float acc[kDecMaxR][8];
 #pragma unroll
   for (int h = 0; h < kDecMaxR; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-#pragma unroll 4
-  for (int j = tid / NC; j < n; j += G) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(vbase + (int64_t)j * p.sv[2] + 8 * c);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int j = tid / NC + i * G;
+    if (j >= n) break;
+    const u32x4 w = vw[i];
     float vv[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
