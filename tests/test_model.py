@@ -264,3 +264,20 @@ def test_tuned_gemm_context_is_inert_without_a_gpu():
     with gt.tuned_gemms():
         x = torch.randn(4, 8) @ torch.randn(8, 3)
     assert x.shape == (4, 3) and gt._load() is False
+
+
+def test_split_k_chunking_and_weight_gradient_on_cpu():
+    pj = importlib.import_module("mega-trading_amd.projection")
+    # the largest of 16, 8, 4, 2 that divides the rows into chunks of >= 1024, else 1
+    assert [pj.split_k_chunks(r) for r in (32768, 16384, 8192, 4096, 3072, 2048, 1024, 1000, 0)] == \
+        [16, 16, 8, 4, 2, 2, 1, 1, 1]
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(3, 1024, 48, generator=g, dtype=torch.float64, requires_grad=True)   # 3072 rows: 2 chunks
+    ws = [torch.randn(o, 48, generator=g, dtype=torch.float64, requires_grad=True) for o in (16, 8)]
+    a, b = pj.project(x, ws)
+    ga, gb = torch.randn_like(a), torch.randn_like(b)
+    torch.autograd.backward((a, b), (ga, gb))
+    x2 = x.detach().reshape(-1, 48)
+    torch.testing.assert_close(ws[0].grad, ga.reshape(-1, 16).t() @ x2)
+    torch.testing.assert_close(ws[1].grad, gb.reshape(-1, 8).t() @ x2)
+    torch.testing.assert_close(x.grad, (ga @ ws[0].detach() + gb @ ws[1].detach()))
