@@ -98,3 +98,10 @@ def test_fused_residual_chain_equals_the_block_loop(autocast):
         # (possibly contracted into an fma): last-ulp fp32 differences that can
         # flip bf16 roundings in the attention backward, which runs in bf16
         assert _rel(a.float(), b.float()) <= 1e-3
+
+
+def test_workload_cli_runs_the_c5_step(capsys):
+    # python -m mega-trading_amd.workload: the command the committed C5 profile was made with
+    assert workload.main(["--route", "hip", "--steps", "1", "--warmup", "1"]) == 0
+    out = capsys.readouterr().out
+    assert "C5 train step, route hip:" in out and "tokens/s" in out
