@@ -20,6 +20,11 @@
   train tokens/sec of the 8-layer decoder with the HIP
   attention in every layer against the same model on the reference's SDPA
   route (the "train tokens/sec" half of the metric).
+* secondary.sdpa: ROCm PyTorch SDPA fwd+bwd (the reference's eager attention,
+  model.py:228-235) on the C2-C4 inputs, with torch's own backend choice and
+  each backend the trainer can force (trainer.py:977-1001), and the aten ops
+  and GPU kernels that ran.  secondary.C5_train adds the attention-only route:
+  the SDPA model with only its attention calls on the HIP op.
 * secondary.C5_generate: KV-cached generation on the HIP kernels against the
   reference's per-token full recompute (model.py:134-147).
 * ops: the decoder operators' HIP kernels (RMSNorm, SwiGLU gate, cross-entropy
@@ -303,6 +308,27 @@ def hbm_traffic(kernel):
     return None
 
 
+def cpu_model_name() -> str:
+    """The host CPU's "Model name" line as lscpu prints it (/proc/cpuinfo's
+    "model name" when lscpu is unavailable)."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
 def cpu_baseline(cfg):
     """Reference CPU attention (torch SDPA fp32 fwd + autograd bwd) on one batch
     element of the workload, 1 warm-up + 3 timed repeats, median."""
@@ -321,14 +347,7 @@ def cpu_baseline(cfg):
             times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    model = cpu_model_name()
     return {
         "value": fwd_bwd_flops(1, t, hq, d) / med / 1e12,
         "unit": "TFLOP/s",
@@ -338,6 +357,101 @@ def cpu_baseline(cfg):
                   f"of the workload (B=1,T={t},Hq={hq},Hkv={hkv},D={d}), median of 3 after 1 warm-up: "
                   f"{med * 1e3:.1f} ms; host '{model}', os.cpu_count()={os.cpu_count()}",
     }
+
+
+SDPA_BACKEND_OPS = {
+    "aten::_scaled_dot_product_flash_attention": "flash",
+    "aten::_scaled_dot_product_efficient_attention": "efficient",
+    "aten::_scaled_dot_product_attention_math": "math",
+    "aten::_scaled_dot_product_cudnn_attention": "cudnn",
+}
+
+
+def sdpa_kernels_used(fn):
+    """Run ``fn`` once under torch.profiler and report which SDPA implementation
+    ran: the aten SDPA entry points dispatched (their names fix the backend)
+    and the GPU kernels whose names mark them as attention kernels."""
+    from torch.autograd import DeviceType
+    from torch.profiler import ProfilerActivity, profile
+
+    torch.cuda.synchronize()
+    ops, kernels = set(), set()
+    try:
+        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+            fn()
+            torch.cuda.synchronize()
+        events = prof.events()
+    except RuntimeError as exc:  # profiler unavailable: report that instead of guessing
+        return {"backend": None, "aten_ops": [], "gpu_kernels": [], "error": str(exc)[:200]}
+    for e in events:
+        name = e.name
+        if name.startswith(("aten::_scaled_dot_product", "aten::_flash_attention", "aten::_efficient_attention")):
+            ops.add(name)
+        elif e.device_type == DeviceType.CUDA and any(s in name.lower() for s in ("attn", "attention", "fmha", "flash")):
+            kernels.add(name[:160])
+    backends = sorted({SDPA_BACKEND_OPS[o] for o in ops if o in SDPA_BACKEND_OPS})
+    return {"backend": "+".join(backends) if backends else None, "aten_ops": sorted(ops), "gpu_kernels": sorted(kernels)}
+
+
+def time_sdpa_steps(cfg, steps, warmup, backend="auto"):
+    """ROCm PyTorch SDPA fwd+bwd (the reference's eager attention, model.py:228-235)
+    on the inputs of time_op_steps: Q and K rotated once beforehand as the
+    reference's RotaryEmbedding does (bf16 tables, model.py:290-294), then
+    ``F.scaled_dot_product_attention(is_causal=True, enable_gqa=...)`` forward
+    plus autograd into (q, k, v), under the trainer's backend context.
+    Returns (ms per step by HIP events, kernels used)."""
+    import torch.nn.functional as F
+
+    pkg = importlib.import_module("mega-trading_amd")
+    wl = pkg.workload
+    b, t, hq, hkv, d = cfg
+    dev = torch.device("cuda:0")
+    q, k, v, do = make_inputs(cfg, dev)
+    cos, sin = rope_tables(t, d, 10_000.0, dev)
+    c16, s16 = cos.to(q.dtype), sin.to(q.dtype)
+    q = pkg.model.rotate(q, c16, s16).detach().requires_grad_(True)
+    k = pkg.model.rotate(k, c16, s16).detach().requires_grad_(True)
+    v = v.detach().requires_grad_(True)
+
+    def step():
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=hq != hkv)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    with wl.attention_kernel_context(backend, dev):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        used = sdpa_kernels_used(step)
+    return start.elapsed_time(end) / steps, used
+
+
+def sdpa_comparators(pkg, configs, steps):
+    """ROCm SDPA fwd+bwd at each named config: torch's own choice ("auto", what
+    the reference's eager route runs) and every backend the trainer can force
+    that accepts the call, each with the kernels that actually ran, beside the
+    HIP op's time on the same inputs."""
+    out = {}
+    for name, cfg in configs.items():
+        b, t, hq, hkv, d = cfg
+        flops = fwd_bwd_flops(b, t, hq, d)
+        row = {}
+        for backend in ("auto", "flash", "efficient", "math"):
+            try:
+                ms, used = time_sdpa_steps(cfg, max(3, steps), 2, backend)
+            except RuntimeError as exc:
+                row[backend] = {"error": str(exc).splitlines()[0][:160]}
+                torch.cuda.synchronize()
+                continue
+            row[backend] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2), **used}
+            torch.cuda.empty_cache()
+        out[name] = row
+    return out
 
 
 def sdpa_backends_usable(d=64, repeats=4):
@@ -362,24 +476,36 @@ def sdpa_backends_usable(d=64, repeats=4):
 
 def train_tokens_per_second(pkg, steps, warmup):
     """the 8-layer decoder train step on the same seeded
-    weights and Zipf batch through three routes:
+    weights and Zipf batch through four routes:
+      attention_only -- the SDPA route unchanged (torch norms, SwiGLU,
+                projections, logits + nn.CrossEntropyLoss as trainer.py:309,
+                336-338, default GEMM selection) except that every attention
+                call (RoPE + SDPA) is the fused-RoPE HIP op: the attention's
+                own contribution, the north-star figure;
+      triton -- the reference's own Triton routing with the HIP kernels in its
+                place (attention + SwiGLU gate + fused loss head; norms stay
+                torch, model.py:166,176);
       hip    -- every HIP operator of this package (attention with fused RoPE,
                 packed SwiGLU gate, RMSNorm) and its projections (q/k/v and
-                w1/w3 each one GEMM, split-K fp32 weight gradients);
-      triton -- the reference's own Triton routing with the HIP kernels in its
-                place (attention + SwiGLU gate; norms stay torch, model.py:166,176);
+                w1/w3 each one GEMM, split-K fp32 weight gradients, tuned GEMMs);
       sdpa   -- the reference's eager route (SDPA + torch ops): the baseline.
+    sdpa_backend records which SDPA implementation the baseline's attention
+    calls ran (from a profiled step).
     """
     wl = pkg.workload
     ids, labels = wl.zipf_batch(wl.C5_BATCH, wl.C5_SEQ, wl.C5_MODEL["vocab_size"])
     out = {}
-    for name, backend in (("hip", "hip"), ("triton", "triton"), ("sdpa", "auto")):
-        model = wl.build_model(backend, seed=0, device="cuda")
+    for name, route in (("hip", "hip"), ("triton", "triton"), ("attention_only", "attention_only"), ("sdpa", "auto")):
+        model = wl.build_model(route, seed=0, device="cuda")
         step = wl.TrainStep(model, ids, labels)
         tps, ms, loss = step.tokens_per_second(steps, warmup)
-        out[name] = {"tokens_per_s": round(tps, 1), "ms_per_step": round(ms, 3), "loss": round(loss, 4)}
+        out[name] = {"tokens_per_s": round(tps, 1), "ms_per_step": round(ms, 3), "loss": round(loss, 4),
+                     "loss_form": step.loss_kind}
+        if name == "sdpa":
+            out["sdpa_backend"] = sdpa_kernels_used(step)
         del step, model
         torch.cuda.empty_cache()
+    out["speedup_attention_only"] = round(out["attention_only"]["tokens_per_s"] / out["sdpa"]["tokens_per_s"], 4)
     out["speedup"] = round(out["hip"]["tokens_per_s"] / out["sdpa"]["tokens_per_s"], 4)
     out["speedup_reference_routing"] = round(out["triton"]["tokens_per_s"] / out["sdpa"]["tokens_per_s"], 4)
     out["sdpa_backends_usable"] = sdpa_backends_usable()
@@ -524,6 +650,12 @@ def main(argv=None) -> int:
             "wall_ms_per_step": round(ms_wall, 4),
         },
     }
+    sdpa = sdpa_comparators(pkg, {"C2": C2, "C3": C3, "C4": C4}, steps=max(5, args.steps // 5))
+    line["secondary"]["sdpa"] = sdpa
+    for name in ("C2", "C3", "C4"):
+        line["secondary"][f"sdpa_{name}_ms"] = sdpa[name]["auto"].get("ms")
+        line["secondary"][f"sdpa_{name}_backend"] = sdpa[name]["auto"].get("backend")
+    line["secondary"]["hip_C2_C3_C4_ms"] = [round(ms_c2, 4), round(ms_event, 4), round(ms_c4, 4)]
     if not args.no_train:
         line["secondary"]["C5_train"] = train_tokens_per_second(pkg, steps=20, warmup=5)
         line["secondary"]["C5_generate"] = generate_tokens_per_second(pkg)

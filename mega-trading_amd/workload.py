@@ -8,23 +8,77 @@ sequences of 1024 token ids drawn i.i.d. from a Zipf(1.1) law over the
 vocabulary ranks, split into inputs and next-token labels as
 ``dataset.py:134-140`` (``tokens_to_example``) does.
 
-A step is what ``trainer.py:333-346`` times: bf16 autocast forward, cross
-entropy, backward, fused AdamW step and ``zero_grad``; tokens/sec counts the
-label tokens of the timed steps over their wall time, synchronised at both
-ends (``trainer.py:686-702``).
+A step is what ``trainer.py:333-346`` times: bf16 autocast forward under
+the attention-backend context (``attention_kernel_context``,
+``trainer.py:977-1001``), cross entropy, backward, fused AdamW step and
+``zero_grad``; tokens/sec counts the label tokens of the timed steps over
+their wall time, synchronised at both ends (``trainer.py:686-702``).
+
+Routes (``build_model``): "auto" / "flash" / "efficient" / "math" are the
+reference's eager SDPA route (the last three force that SDPA kernel);
+"attention_only" is that route with only the attention call -- RoPE plus
+SDPA -- replaced by the fused-RoPE HIP op; "triton" is the reference's
+Triton routing (attention, SwiGLU gate and fused loss head on HIP kernels);
+"hip" is this package's fullest route.
 """
 
 from __future__ import annotations
 
+import contextlib
 import gc
 import time
+from typing import Iterator
 
 import numpy as np
 import torch
+from torch import nn
 
-from .model import TradingModel
+from .model import HIP_BACKENDS, TradingModel
 
-__all__ = ["C5_MODEL", "C5_BATCH", "C5_SEQ", "zipf_batch", "build_model", "TrainStep"]
+__all__ = ["C5_MODEL", "C5_BATCH", "C5_SEQ", "ROUTES", "zipf_batch", "build_model", "TrainStep",
+           "attention_kernel_context"]
+
+# train-step routes: the model's attention_backend values plus "attention_only"
+ROUTES = ("auto", "flash", "efficient", "math", "attention_only", "triton", "hip")
+
+
+@contextlib.contextmanager
+def attention_kernel_context(backend: str, device) -> Iterator[None]:
+    """The trainer's SDPA backend selection (``trainer.py:977-1001``).
+
+    "auto", "triton" (and this package's "hip" / "attention_only") leave
+    torch's choice alone; "flash", "efficient" and "math" restrict
+    ``F.scaled_dot_product_attention`` to that one kernel for the duration
+    (``torch.nn.attention.sdpa_kernel``; the older
+    ``torch.backends.cuda.sdp_kernel`` flags where that API is missing), so a
+    call the forced kernel cannot serve raises instead of falling back.  They
+    require a GPU device, as the reference's do."""
+    if backend in {"auto", "triton", "hip", "attention_only"}:
+        yield
+        return
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise RuntimeError(f"{backend} attention backend requires CUDA")
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        mapping = {
+            "flash": SDPBackend.FLASH_ATTENTION,
+            "efficient": SDPBackend.EFFICIENT_ATTENTION,
+            "math": SDPBackend.MATH,
+        }
+        selected = mapping[backend]
+    except (ImportError, AttributeError):
+        flags = {
+            "flash": dict(enable_flash=True, enable_mem_efficient=False, enable_math=False),
+            "efficient": dict(enable_flash=False, enable_mem_efficient=True, enable_math=False),
+            "math": dict(enable_flash=False, enable_mem_efficient=False, enable_math=True),
+        }
+        with torch.backends.cuda.sdp_kernel(**flags[backend]):
+            yield
+        return
+    with sdpa_kernel(selected):
+        yield
 
 C5_MODEL = dict(
     vocab_size=16384,
@@ -52,32 +106,65 @@ def zipf_batch(batch: int, seq_len: int, vocab: int, *, exponent: float = 1.1, s
     return ids[:, :-1].contiguous(), ids[:, 1:].contiguous()
 
 
-def build_model(attention_backend: str, *, seed: int = 0, device="cuda", **overrides) -> TradingModel:
-    """C5 model (or a variant via ``overrides``) with seeded N(0, 0.02) weights, fp32 master copy."""
+def build_model(route: str, *, seed: int = 0, device="cuda", **overrides) -> TradingModel:
+    """C5 model (or a variant via ``overrides``) with seeded N(0, 0.02) weights, fp32 master copy.
+
+    ``route`` is an ``attention_backend`` value, or "attention_only": the
+    "auto" (SDPA) model -- torch norms, SwiGLU, projections and loss head --
+    whose attention layers alone call the fused-RoPE HIP op (the same weights
+    for the same seed)."""
+    if route not in ROUTES:
+        raise ValueError("route must be one of: " + ", ".join(ROUTES))
     cfg = dict(C5_MODEL)
     cfg.update(overrides)
     torch.manual_seed(seed)
-    return TradingModel(attention_backend=attention_backend, **cfg).to(device)
+    model = TradingModel(attention_backend="auto" if route == "attention_only" else route, **cfg).to(device)
+    if route == "attention_only":
+        for block in model.blocks:
+            # LlamaAttention routes "triton" with dropout 0 to the HIP op (model.py:224-226)
+            # and keeps the three nn.Linear projections and o_proj of the SDPA route
+            block.attention.attention_backend = "triton"
+    model.route = route
+    return model
 
 
 class TrainStep:
-    """One optimisation step of ``model`` on a fixed batch (bf16 autocast, fused AdamW)."""
+    """One optimisation step of ``model`` on a fixed batch (bf16 autocast, fused AdamW).
 
-    def __init__(self, model: TradingModel, input_ids: torch.Tensor, labels: torch.Tensor, *, lr: float = 3e-4):
+    ``loss="trainer"`` computes the loss as the reference trainer does
+    (``trainer.py:309,336-338``): logits from ``model(input_ids)``, then
+    ``nn.CrossEntropyLoss`` on the flattened logits, under the attention
+    backend context.  ``loss="model"`` uses the model's loss entry
+    (``forward_with_loss``, ``model.py:84-131``), where the "triton" / "hip"
+    routes take the fused linear cross-entropy head; for the SDPA route the
+    two are the same computation.  The default is "model" for the HIP routes
+    and "trainer" otherwise."""
+
+    def __init__(self, model: TradingModel, input_ids: torch.Tensor, labels: torch.Tensor, *, lr: float = 3e-4,
+                 loss: str | None = None):
         self.model = model
         dev = next(model.parameters()).device
         self.input_ids = input_ids.to(dev)
         self.labels = labels.to(dev)
         self.optimizer = torch.optim.AdamW(model.parameters(), lr=lr, fused=dev.type == "cuda")
         self.device = dev
+        self.backend = model.operator_backend
+        if loss is None:
+            loss = "model" if self.backend in HIP_BACKENDS else "trainer"
+        if loss not in ("model", "trainer"):
+            raise ValueError('loss must be "model" or "trainer"')
+        self.loss_kind = loss
+        self.loss_fn = nn.CrossEntropyLoss()
 
     def __call__(self) -> torch.Tensor:
-        # the model's loss entry (model.py:84-131): for the "auto"/SDPA route it is
-        # exactly the trainer's logits + nn.CrossEntropyLoss (trainer.py:309,337-338);
-        # the "triton"/"hip" routes take the fused linear cross-entropy head there
         self.model.train()
-        with torch.autocast(device_type=self.device.type, dtype=torch.bfloat16):
-            loss, _ = self.model.forward_with_loss(self.input_ids, self.labels, return_logits=False)
+        with torch.autocast(device_type=self.device.type, dtype=torch.bfloat16), \
+                attention_kernel_context(self.backend, self.device):
+            if self.loss_kind == "trainer":
+                logits = self.model(self.input_ids)
+                loss = self.loss_fn(logits.reshape(-1, logits.shape[-1]), self.labels.reshape(-1))
+            else:
+                loss, _ = self.model.forward_with_loss(self.input_ids, self.labels, return_logits=False)
         loss.backward()
         self.optimizer.step()
         self.optimizer.zero_grad(set_to_none=True)
@@ -114,7 +201,8 @@ def main(argv=None) -> int:
     import argparse
 
     ap = argparse.ArgumentParser(description=main.__doc__)
-    ap.add_argument("--route", default="hip", help='attention backend: "hip", "triton" or "auto" (SDPA)')
+    ap.add_argument("--route", default="hip", choices=ROUTES,
+                    help='"hip", "triton", "attention_only", or an SDPA route ("auto", "flash", "efficient", "math")')
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=3)
     args = ap.parse_args(argv)

@@ -36,7 +36,7 @@ def _rel(a, b):
     return ((a - b).norm() / b.norm().clamp_min(1e-12)).item()
 
 
-@pytest.mark.parametrize("backend,fuse", [("hip", True), ("triton", True), ("hip", False)])
+@pytest.mark.parametrize("backend,fuse", [("hip", True), ("triton", True), ("hip", False), ("attention_only", True)])
 def test_hip_route_matches_sdpa_route(backend, fuse):
     ids, labels = workload.zipf_batch(2, 384, SMALL["vocab_size"], seed=1)
     ids, labels = ids.cuda(), labels.cuda()
@@ -105,3 +105,36 @@ def test_workload_cli_runs_the_c5_step(capsys):
     assert workload.main(["--route", "hip", "--steps", "1", "--warmup", "1"]) == 0
     out = capsys.readouterr().out
     assert "C5 train step, route hip:" in out and "tokens/s" in out
+
+
+@pytest.mark.parametrize("backend,op", [("math", "aten::_scaled_dot_product_attention_math"),
+                                        ("efficient", "aten::_scaled_dot_product_efficient_attention")])
+def test_forced_sdpa_backend_dispatches_that_kernel(backend, op):
+    """trainer.py:977-1001 restated: inside the context SDPA runs the forced kernel
+    (seen in the dispatched aten op), or raises when that kernel cannot serve the
+    call; outside it torch chooses freely again."""
+    from torch.profiler import ProfilerActivity, profile
+
+    q = torch.randn(2, 8, 256, 64, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(2, 2, 256, 64, device="cuda", dtype=torch.bfloat16)
+    try:
+        with workload.attention_kernel_context(backend, "cuda"), profile(activities=[ProfilerActivity.CPU]) as prof:
+            torch.nn.functional.scaled_dot_product_attention(q, k, k, is_causal=True, enable_gqa=True)
+            torch.cuda.synchronize()
+    except RuntimeError as exc:
+        pytest.skip(f"{backend} SDPA kernel refuses a causal GQA bf16 call on this build: {exc}")
+    names = {e.name for e in prof.events()}
+    assert op in names, sorted(n for n in names if "scaled_dot" in n)
+
+
+def test_attention_only_train_step_runs_with_the_trainer_loss():
+    ids, labels = workload.zipf_batch(2, 256, SMALL["vocab_size"], seed=5)
+    losses = {}
+    for route in ("auto", "attention_only"):
+        m = workload.build_model(route, seed=0, device="cuda", **SMALL)
+        step = workload.TrainStep(m, ids, labels)
+        assert step.loss_kind == "trainer"
+        losses[route] = [float(step()) for _ in range(3)]
+    print("losses", losses)
+    for a, b in zip(losses["attention_only"], losses["auto"]):
+        assert abs(a - b) <= TOL_LOSS_REL * abs(b)
