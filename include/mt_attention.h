@@ -104,6 +104,29 @@ int mt_gqa_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
                     const float* rope_cos, const float* rope_sin, void* stream);
 
 /*
+ * Allocation-free backward.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  Same arguments and
+ * results as mt_gqa_attn_bwd without the workspace: the delta / LSE vectors
+ * and the dK/dV partial sums live in a fixed device array of
+ * MT_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends.  The dK/dV head split is mt_gqa_attn_bwd's when its partials
+ * fit (then the results are bit-identical), else the largest smaller one that
+ * fits; a shape whose delta and LSE vectors alone (8 * B * Hq * T bytes,
+ * rounded up) exceed the array returns MT_E_WORKSPACE before any device call.
+ * Nothing in the array needs to start at zero: every value read was written
+ * earlier in the same call.  All calls on one GPU share that GPU's array, so
+ * calls that overlap in time on one GPU (other streams, other threads) race;
+ * serialise them.  Calls no hipMalloc / hipFree.  The stream, when given,
+ * must belong to the current device.
+ */
+#define MT_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int mt_gqa_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                            const void* dout, void* dq, void* dk, void* dv, int B, int Hq, int Hkv, int T, int D,
+                            const int64_t* strides, float scale, int dtype, const float* rope_cos,
+                            const float* rope_sin, void* stream);
+
+/*
  * The two halves of mt_gqa_attn_bwd, for callers that schedule or time the
  * backward kernels separately (same arguments and conventions).
  *   mt_gqa_attn_bwd_dq  <- _triton_attention_backward_dq_server_kernel launch,

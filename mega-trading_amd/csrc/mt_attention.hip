@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/mt_attention.h"
 #include "attn_kernels.h"
@@ -118,13 +119,17 @@ int choose_split(int B, int Hq, int Hkv, int T, int D) {
 size_t vec_bytes(int B, int Hq, int T) { return (((size_t)B * Hq * T * sizeof(float)) + 255) / 256 * 256; }
 size_t delta_bytes(int B, int Hq, int T) { return 2 * vec_bytes(B, Hq, T); }
 
-size_t workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
-  const int split = choose_split(B, Hq, Hkv, T, D);
+size_t workspace_bytes_split(int B, int Hq, int Hkv, int T, int D, int split) {
   const size_t part = split > 1 ? (size_t)split * 2 * B * Hkv * T * D * sizeof(float) : 0;
   return delta_bytes(B, Hq, T) + part;
 }
 
-void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, float scale) {
+size_t workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return workspace_bytes_split(B, Hq, Hkv, T, D, choose_split(B, Hq, Hkv, T, D));
+}
+
+// split = 0: the dK/dV head split of choose_split; else that split (a divisor of R)
+void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, float scale, int split = 0) {
   p.B = B;
   p.Hq = Hq;
   p.Hkv = Hkv;
@@ -136,7 +141,7 @@ void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, floa
   p.nqb = (T + mt::kBlk - 1) / mt::kBlk;
   p.nsb = (p.nqb + p.rb - 1) / p.rb;
   p.nkb = (T + kv_keys(D) - 1) / kv_keys(D);
-  p.n_split = choose_split(B, Hq, Hkv, T, D);
+  p.n_split = split > 0 ? split : choose_split(B, Hq, Hkv, T, D);
   p.scale = scale;
   p.scale_log2 = scale * mt::kLog2e;
 }
@@ -224,14 +229,15 @@ Launcher pick(int dtype, int D, bool rope) {
 int bwd_impl(int stage, const void* q, const void* k, const void* v, const void* o, const float* lse,
              const void* dout, void* dq, void* dk, void* dv, void* workspace, size_t workspace_size,
              int B, int Hq, int Hkv, int T, int D, const int64_t* strides, float scale, int dtype,
-             const float* rope_cos, const float* rope_sin, void* stream) {
+             const float* rope_cos, const float* rope_sin, void* stream, int split = 0) {
   int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
   if (rc) return rc;
   if (!strides) return fail(MT_E_NULL, "strides is NULL");
   if (!lse) return fail(MT_E_NULL, "lse is NULL");
   if (!workspace) return fail(MT_E_NULL, "workspace is NULL");
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(MT_E_STRIDE, "workspace must be 256-byte aligned");
-  const size_t need = workspace_bytes(B, Hq, Hkv, T, D);
+  if (split <= 0) split = choose_split(B, Hq, Hkv, T, D);
+  const size_t need = workspace_bytes_split(B, Hq, Hkv, T, D, split);
   if (workspace_size < need)
     return fail(MT_E_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", workspace_size, need);
   if ((rc = check_tensor("q", q, strides + 0))) return rc;
@@ -266,7 +272,7 @@ int bwd_impl(int stage, const void* q, const void* k, const void* v, const void*
   copy3(p.sout, strides + 20);
   copy3(p.sdk, strides + 24);
   copy3(p.sdv, strides + 28);
-  fill_geometry(p, B, Hq, Hkv, T, D, scale);
+  fill_geometry(p, B, Hq, Hkv, T, D, scale, split);
   hipError_t e = pick<false>(dtype, D, rope_cos != nullptr)(p, static_cast<hipStream_t>(stream), stage);
   if (e != hipSuccess) return fail(int(e), "backward launch failed: %s", hipGetErrorString(e));
   return ok();
@@ -274,9 +280,47 @@ int bwd_impl(int stage, const void* q, const void* k, const void* v, const void*
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Allocation-free backward: the workspace lives in a fixed device array.
+// ---------------------------------------------------------------------------
+// Every GPU the library runs on holds its own copy of this array (64 MiB,
+// zero-initialised at module load) until the process ends.  In host code
+// `scratch` names a host-side stand-in, not device memory: its device address
+// is looked up once per device with hipGetSymbolAddress and only that address
+// is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[MT_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch` (looked up on the first
+// call per device, with that device current).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(int(e), "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MT_E_SHAPE, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(e != hipSuccess ? int(e) : MT_E_NULL, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MT_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
-int mt_version(void) { return (0 << 16) | 4; }
+int mt_version(void) { return (0 << 16) | 5; }
 
 const char* mt_last_error(void) { return mt_abi::last_error(); }
 
@@ -341,6 +385,37 @@ int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float*
       rope_cos, rope_sin, stream
 
 int mt_gqa_attn_bwd(MT_BWD_ARGS) { return bwd_impl(3, MT_BWD_PASS); }
+
+int mt_gqa_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                            const void* dout, void* dq, void* dk, void* dv, int B, int Hq, int Hkv, int T, int D,
+                            const int64_t* strides, float scale, int dtype, const float* rope_cos,
+                            const float* rope_sin, void* stream) {
+  // shape checks first: a shape that does not fit is rejected before any device call
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
+  if (rc) return rc;
+  // the standard head split when its partials fit, else the largest smaller
+  // divisor of R that fits (split 1 keeps only delta and LSE)
+  const int R = Hq / Hkv;
+  int split = choose_split(B, Hq, Hkv, T, D);
+  while (split > 1 && (R % split || workspace_bytes_split(B, Hq, Hkv, T, D, split) > MT_NOALLOC_SCRATCH_BYTES))
+    --split;
+  const size_t need = workspace_bytes_split(B, Hq, Hkv, T, D, split);
+  if (need > MT_NOALLOC_SCRATCH_BYTES)
+    return fail(MT_E_WORKSPACE,
+                "shape B=%d Hq=%d T=%d needs %zu bytes of backward scratch; the allocation-free backward holds "
+                "at most %zu (use mt_gqa_attn_bwd with a workspace)",
+                B, Hq, T, need, (size_t)MT_NOALLOC_SCRATCH_BYTES);
+  if (stream) {
+    int sdev = -1, cur = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) == hipSuccess && hipGetDevice(&cur) == hipSuccess &&
+        sdev != cur)
+      return fail(MT_E_SHAPE, "stream belongs to device %d but device %d is current", sdev, cur);
+  }
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  return bwd_impl(3, q, k, v, o, lse, dout, dq, dk, dv, ws, MT_NOALLOC_SCRATCH_BYTES, B, Hq, Hkv, T, D, strides,
+                  scale, dtype, rope_cos, rope_sin, stream, split);
+}
 int mt_gqa_attn_bwd_dq(MT_BWD_ARGS) { return bwd_impl(1, MT_BWD_PASS); }
 int mt_gqa_attn_bwd_dkv(MT_BWD_ARGS) { return bwd_impl(2, MT_BWD_PASS); }
 

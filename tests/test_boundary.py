@@ -30,7 +30,23 @@ def test_library_exports_every_declared_symbol(mta):
     assert declared == sorted(mta._native.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/mt_attention.h but not exported"
-    assert lib.mt_version() == (0 << 16) | 4
+    assert lib.mt_version() == (0 << 16) | 5
+
+
+def test_noalloc_backward_rejects_shapes_beyond_its_scratch(mta):
+    """mt_gqa_attn_bwd_noalloc: a shape whose delta / LSE vectors alone exceed
+    the fixed 64 MiB scratch fails with MT_E_WORKSPACE before any device call
+    (the pointers are never dereferenced)."""
+    lib = mta._native.load()
+    p = 0x10000
+    s = (ctypes.c_int64 * 32)(*([0, 0, 64, 1] * 8))
+    # 8 * B * Hq * T bytes of vectors: B=64, Hq=64, T=4096 -> 128 MiB
+    rc = lib.mt_gqa_attn_bwd_noalloc(p, p, p, p, p, p, p, p, p, 64, 64, 16, 4096, 64, s, 0.125, 0, None, None, None)
+    assert rc == -6
+    assert b"at most 67108864" in lib.mt_last_error()
+    # shape errors keep their own codes
+    assert lib.mt_gqa_attn_bwd_noalloc(p, p, p, p, p, p, p, p, p, 1, 6, 4, 16, 64, s, 0.125, 0, None, None, None) == -2
+    assert lib.mt_gqa_attn_bwd_noalloc(p, p, p, p, p, p, p, p, p, 1, 4, 2, 16, 48, s, 0.125, 0, None, None, None) == -2
 
 
 def test_probe_library_exports_the_mfma_probe():
