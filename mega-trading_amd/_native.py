@@ -13,6 +13,9 @@ import threading
 
 LIB_NAME = "libmt_attn.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# the GPU implementations of the mega_trading_amd attention ops (PyTorch-ROCm side, links libmt_attn.so)
+TORCH_OPS_NAME = "libmt_torch.so"
+TORCH_OPS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), TORCH_OPS_NAME)
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -88,20 +91,29 @@ def library_path() -> str:
     return LIB_PATH
 
 
+def torch_ops_path() -> str:
+    return TORCH_OPS_PATH
+
+
 def load() -> ctypes.CDLL:
-    """Load libmt_attn.so (once) and declare the C signatures."""
+    """Load libmt_attn.so (once) and declare the C signatures; also load
+    libmt_torch.so, which registers the attention ops' GPU kernels with torch."""
     global _lib
     if _lib is not None:
         return _lib
     with _lock:
         if _lib is not None:
             return _lib
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(
-                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
-                "(or python mega-trading_amd/build_lib.py) before using the HIP attention op"
-            )
+        for path in (LIB_PATH, TORCH_OPS_PATH):
+            if not os.path.exists(path):
+                raise RuntimeError(
+                    f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                    "(or python mega-trading_amd/build_lib.py) before using the HIP attention op"
+                )
         lib = ctypes.CDLL(LIB_PATH)
+        import torch
+
+        torch.ops.load_library(TORCH_OPS_PATH)
         lib.mt_version.restype = _I
         lib.mt_version.argtypes = []
         lib.mt_last_error.restype = ctypes.c_char_p

@@ -9,11 +9,14 @@ interleaved RoPE that ``model.py:223`` applies right before the attention call
 (``triton_apply_rope``, ``src/mega_trading/kernels/triton_ops.py:45-54``) into
 the kernels' Q/K tile loads.
 
-Both ops are ``torch.library`` custom ops (``mega_trading_amd::gqa_attn_fwd``
-and ``::gqa_attn_bwd``) with fake implementations, so ``torch.compile`` treats
-them as opaque nodes.  They launch on the caller's current stream, never
-synchronise and never fall back to another implementation: without the HIP
-library they raise.
+The attention ops are ``torch.library`` ops (``mega_trading_amd::gqa_attn_fwd``,
+``::gqa_rope_attn_fwd``, ``::gqa_attn_bwd`` and the packed q|k|v pair) whose
+schemas, fake implementations and autograd are declared here, so
+``torch.compile`` treats them as opaque nodes; their GPU implementations live
+in ``libmt_torch.so`` (``csrc/mt_torch.cpp``), which prepares the arguments,
+allocates the outputs and calls the C ABI of ``libmt_attn.so`` on the
+caller's current stream.  They never synchronise and never fall back to
+another implementation: without the HIP libraries they raise.
 """
 
 from __future__ import annotations
@@ -97,6 +100,7 @@ def rope_attention_packed(
     _validate(q, k, v, heads // kv_heads)
     c, s = _rope_tables(cos, sin, q)
     d = q.shape[-1]
+    _native.load()
     out, _lse, _q_rot, _k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_packed_fwd(
         qkv, c, s, heads, kv_heads, 1.0 / math.sqrt(d))
     return out
@@ -271,6 +275,7 @@ def _forward(q, k, v, cos, sin):
     if q.dtype == torch.float32:
         o, lse = _forward(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), cos, sin)
         return o.to(torch.float32), lse
+    _native.load()
     scale = 1.0 / math.sqrt(q.shape[-1])
     if cos is None:
         return torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, v, scale)
@@ -278,52 +283,32 @@ def _forward(q, k, v, cos, sin):
     return out, lse
 
 
-def _launch_fwd(q, k, v, cos, sin, scale, out=None):
-    lib = _native.load()
-    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-    b, hq, t, d = q.shape
-    hkv = k.shape[1]
-    if out is None:
-        out = _kernel_ready(torch.empty_like(q))
-    lse = torch.empty((b, hq, t), device=q.device, dtype=torch.float32)
-    q_rot = k_rot = None
-    if cos is not None:
-        q_rot = torch.empty((b, hq, t, d), device=q.device, dtype=q.dtype)
-        k_rot = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
-    strides = _strides(q, k, v, out)
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = lib.mt_gqa_attn_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(), _ptr(q_rot), _ptr(k_rot),
-            b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
-        )
-    _native.check(rc, "mt_gqa_attn_fwd")
-    return out, lse, q_rot, k_rot
-
-
 # ---------------------------------------------------------------------------
-# custom ops
+# the attention ops: schemas and shapes here, GPU kernels in libmt_torch.so
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("mega_trading_amd::gqa_attn_fwd", mutates_args=(), device_types="cuda")
-def gqa_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> tuple[torch.Tensor, torch.Tensor]:
-    out, lse, _, _ = _launch_fwd(q, k, v, None, None, scale)
-    return out, lse
+_LIB = torch.library.Library("mega_trading_amd", "FRAGMENT")
+_LIB.define("gqa_attn_fwd(Tensor q, Tensor k, Tensor v, float scale) -> (Tensor, Tensor)")
+# returns (out, lse, q_rot, k_rot); q_rot / k_rot feed the backward
+_LIB.define("gqa_rope_attn_fwd(Tensor q, Tensor k, Tensor v, Tensor cos, Tensor sin, float scale) "
+            "-> (Tensor, Tensor, Tensor, Tensor)")
+# gradients w.r.t. (q, k, v); with RoPE tables q and k are the forward's
+# rotated tensors and dQ / dK come back in the un-rotated basis
+_LIB.define("gqa_attn_bwd(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? cos, "
+            "Tensor? sin, float scale) -> (Tensor, Tensor, Tensor)")
+# (out [B, T, Hq*D], lse, q_rot, k_rot) for a packed qkv
+_LIB.define("gqa_rope_attn_packed_fwd(Tensor qkv, Tensor cos, Tensor sin, int hq, int hkv, float scale) "
+            "-> (Tensor, Tensor, Tensor, Tensor)")
+# gradient w.r.t. the packed qkv (un-rotated basis), in qkv's layout
+_LIB.define("gqa_attn_bwd_packed(Tensor q_rot, Tensor k_rot, Tensor qkv, Tensor out, Tensor lse, Tensor dout, "
+            "Tensor cos, Tensor sin, int hq, int hkv, float scale) -> Tensor")
 
 
-@gqa_attn_fwd.register_fake
+@torch.library.register_fake("mega_trading_amd::gqa_attn_fwd")
 def _gqa_attn_fwd_fake(q, k, v, scale):
     return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
 
 
-@torch.library.custom_op("mega_trading_amd::gqa_rope_attn_fwd", mutates_args=(), device_types="cuda")
-def gqa_rope_attn_fwd(
-    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, scale: float
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Returns (out, lse, q_rot, k_rot); q_rot/k_rot feed the backward."""
-    return _launch_fwd(q, k, v, cos, sin, scale)
-
-
-@gqa_rope_attn_fwd.register_fake
+@torch.library.register_fake("mega_trading_amd::gqa_rope_attn_fwd")
 def _gqa_rope_attn_fwd_fake(q, k, v, cos, sin, scale):
     b, hq, t, d = q.shape
     return (
@@ -334,68 +319,12 @@ def _gqa_rope_attn_fwd_fake(q, k, v, cos, sin, scale):
     )
 
 
-@torch.library.custom_op("mega_trading_amd::gqa_attn_bwd", mutates_args=(), device_types="cuda")
-def gqa_attn_bwd(
-    q: torch.Tensor,
-    k: torch.Tensor,
-    v: torch.Tensor,
-    o: torch.Tensor,
-    lse: torch.Tensor,
-    dout: torch.Tensor,
-    cos: Optional[torch.Tensor],
-    sin: Optional[torch.Tensor],
-    scale: float,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Gradients w.r.t. (q, k, v).  With RoPE tables, q and k are the rotated
-    tensors of the forward and dQ/dK come back in the un-rotated basis."""
-    b, hq, t, d = q.shape
-    hkv = k.shape[1]
-    dq = torch.empty((b, hq, t, d), device=q.device, dtype=q.dtype)
-    dk = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
-    dv = torch.empty((b, hkv, t, d), device=q.device, dtype=q.dtype)
-    _launch_bwd(q, k, v, o, lse, dout, cos, sin, scale, dq, dk, dv)
-    return dq, dk, dv
-
-
-def _launch_bwd(q, k, v, o, lse, dout, cos, sin, scale, dq, dk, dv):
-    """dq/dk/dv: outputs of q/k/v's shapes, any kernel-ready strides."""
-    lib = _native.load()
-    q, k, v, o = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(o)
-    dout = _kernel_ready(dout.to(q.dtype))
-    lse = lse.contiguous()
-    b, hq, t, d = q.shape
-    hkv = k.shape[1]
-    strides = _strides(q, k, v, o, dout, dq, dk, dv)
-    with torch.cuda.device(q.device):
-        ws_bytes = lib.mt_gqa_attn_bwd_workspace_size(b, hq, hkv, t, d)
-        workspace = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        rc = lib.mt_gqa_attn_bwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), dout.data_ptr(),
-            dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), workspace.data_ptr(), ws_bytes,
-            b, hq, hkv, t, d, strides, scale, _KERNEL_DTYPES[q.dtype], _ptr(cos), _ptr(sin), stream,
-        )
-    _native.check(rc, "mt_gqa_attn_bwd")
-
-
-@gqa_attn_bwd.register_fake
+@torch.library.register_fake("mega_trading_amd::gqa_attn_bwd")
 def _gqa_attn_bwd_fake(q, k, v, o, lse, dout, cos, sin, scale):
     return q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape)
 
 
-@torch.library.custom_op("mega_trading_amd::gqa_rope_attn_packed_fwd", mutates_args=(), device_types="cuda")
-def gqa_rope_attn_packed_fwd(
-    qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, hq: int, hkv: int, scale: float
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Returns (out [B, T, Hq*D], lse, q_rot, k_rot) for a packed qkv."""
-    q, k, v = _packed_views(qkv, hq, hkv)
-    b, _, t, d = q.shape
-    out = torch.empty((b, t, hq, d), device=qkv.device, dtype=qkv.dtype)
-    _out, lse, q_rot, k_rot = _launch_fwd(q, k, v, cos, sin, scale, out=out.transpose(1, 2))
-    return out.view(b, t, hq * d), lse, q_rot, k_rot
-
-
-@gqa_rope_attn_packed_fwd.register_fake
+@torch.library.register_fake("mega_trading_amd::gqa_rope_attn_packed_fwd")
 def _gqa_rope_attn_packed_fwd_fake(qkv, cos, sin, hq, hkv, scale):
     b, t, width = qkv.shape
     d = width // (hq + 2 * hkv)
@@ -403,24 +332,7 @@ def _gqa_rope_attn_packed_fwd_fake(qkv, cos, sin, hq, hkv, scale):
             qkv.new_empty((b, hq, t, d)), qkv.new_empty((b, hkv, t, d)))
 
 
-@torch.library.custom_op("mega_trading_amd::gqa_attn_bwd_packed", mutates_args=(), device_types="cuda")
-def gqa_attn_bwd_packed(
-    q_rot: torch.Tensor, k_rot: torch.Tensor, qkv: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
-    dout: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, hq: int, hkv: int, scale: float,
-) -> torch.Tensor:
-    """Gradient w.r.t. the packed qkv (un-rotated basis), in qkv's layout."""
-    _q, _k, v = _packed_views(qkv, hq, hkv)
-    b, t, _ = qkv.shape
-    d = v.shape[-1]
-    dqkv = torch.empty((b, t, qkv.shape[-1]), device=qkv.device, dtype=qkv.dtype)
-    dq, dk, dv = _packed_views(dqkv, hq, hkv)
-    o = out.view(b, t, hq, d).transpose(1, 2)
-    do = dout.reshape(b, t, hq, d).transpose(1, 2)
-    _launch_bwd(q_rot, k_rot, v, o, lse, do, cos, sin, scale, dq, dk, dv)
-    return dqkv
-
-
-@gqa_attn_bwd_packed.register_fake
+@torch.library.register_fake("mega_trading_amd::gqa_attn_bwd_packed")
 def _gqa_attn_bwd_packed_fake(q_rot, k_rot, qkv, out, lse, dout, cos, sin, hq, hkv, scale):
     return qkv.new_empty(qkv.shape)
 
@@ -552,6 +464,8 @@ def _packed_backward(ctx, grad_out, _grad_lse, _grad_q_rot, _grad_k_rot):
     return dqkv, None, None, None, None, None
 
 
-gqa_attn_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
-gqa_rope_attn_packed_fwd.register_autograd(_packed_backward, setup_context=_packed_setup_context)
-gqa_rope_attn_fwd.register_autograd(_rope_fwd_backward, setup_context=_rope_fwd_setup_context)
+torch.library.register_autograd("mega_trading_amd::gqa_attn_fwd", _fwd_backward, setup_context=_fwd_setup_context)
+torch.library.register_autograd("mega_trading_amd::gqa_rope_attn_packed_fwd", _packed_backward,
+                                setup_context=_packed_setup_context)
+torch.library.register_autograd("mega_trading_amd::gqa_rope_attn_fwd", _rope_fwd_backward,
+                                setup_context=_rope_fwd_setup_context)

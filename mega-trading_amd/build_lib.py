@@ -1,10 +1,16 @@
-"""Build libmt_attn.so (and the bench-only libmt_probe.so) in-tree for gfx950 with hipcc.
+"""Build libmt_attn.so, libmt_torch.so (and the bench-only libmt_probe.so) in-tree.
 
 Run as ``python mega-trading_amd/build_lib.py`` or through
 ``__graft_entry__.build()``.  The libraries land next to this file so they
 travel with the source tree (they are git-ignored, not installed anywhere).
-libmt_probe.so holds a sustained-MFMA-rate probe that bench.py reports beside
-the roofline; it is not part of the attention ABI.
+
+* libmt_attn.so: the gfx950 kernels and their C ABI (hipcc).
+* libmt_torch.so: the PyTorch-ROCm side of the attention ops -- the GPU
+  implementations of the ``mega_trading_amd::*`` ops whose schemas, shapes
+  and autograd ``attention.py`` declares -- built with the host compiler
+  against torch's headers and linked to libmt_attn.so; no device code.
+* libmt_probe.so: a sustained-MFMA-rate probe that bench.py reports beside
+  the roofline; it is not part of the attention ABI.
 """
 
 from __future__ import annotations
@@ -49,10 +55,49 @@ def compile_command(out: str = LIB_PATH, sources: list[str] | None = None) -> li
     ]
 
 
+TORCH_OPS_NAME = "libmt_torch.so"
+TORCH_OPS_PATH = os.path.join(HERE, TORCH_OPS_NAME)
+TORCH_OPS_SOURCES = ["mt_torch.cpp"]
+
+
+def torch_ops_command(out: str = TORCH_OPS_PATH) -> list[str]:
+    import torch
+
+    tdir = os.path.dirname(torch.__file__)
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return [
+        shutil.which("g++") or "g++",
+        "-O2", "-std=c++17", "-fPIC", "-shared",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        "-I", os.path.join(tdir, "include"),
+        "-I", os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+        "-I", os.path.join(rocm, "include"),
+        *[os.path.join(CSRC, s) for s in TORCH_OPS_SOURCES],
+        "-L", os.path.join(tdir, "lib"), "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+        "-L", HERE, "-l:" + LIB_NAME,
+        "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(tdir, "lib"),
+        "-o", out,
+    ]
+
+
 def build(verbose: bool = False) -> str:
-    """Compile both libraries (always; a stale build is never reused)."""
+    """Compile every library (always; a stale build is never reused)."""
     _compile(PROBE_PATH, PROBE_SOURCES, verbose)
-    return _compile(LIB_PATH, SOURCES, verbose)
+    path = _compile(LIB_PATH, SOURCES, verbose)
+    _run(TORCH_OPS_PATH, torch_ops_command(TORCH_OPS_PATH + ".tmp"), verbose)
+    return path
+
+
+def _run(path: str, cmd: list[str], verbose: bool) -> str:
+    tmp = path + ".tmp"
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{cmd[0]} failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, path)
+    return path
 
 
 def _compile(path: str, sources: list[str], verbose: bool) -> str:

@@ -35,6 +35,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _native
 from .attention import _rope_tables
 from .attention import attention as _hip_attention
 from .attention import decode_attention as _hip_decode_attention
@@ -396,6 +397,7 @@ class LlamaAttention(nn.Module):
         kdt = query.dtype if query.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
         q16, k16, v16 = query.to(kdt), key.to(kdt), value.to(kdt)
         cos, sin = _rope_tables(self.rope.cos, self.rope.sin, q16)
+        _native.load()
         out, _lse, _q_rot, k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(
             q16, k16, v16, cos, sin, 1.0 / math.sqrt(self.head_dim))
         shape = (b, self.kv_heads, capacity, self.head_dim)

@@ -224,3 +224,4 @@ def test_native_library_is_loaded(mta):
     mta._native.load()
     maps = open("/proc/self/maps").read()
     assert mta._native.library_path() in maps
+    assert mta._native.torch_ops_path() in maps
