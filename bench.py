@@ -64,8 +64,11 @@ C4 = (8, 2048, 32, 8, 128)
 # algorithmic MFMA FLOPs per launch, in units of B * Hq * D * T(T+1)/2
 KERNEL_FLOP_UNITS = {
     "attn_fwd_kernel": 4,      # S = QK^T, O = PV
-    "attn_bwd_dq_kernel": 6,   # S, dP recomputed; dQ = dS K
-    "attn_bwd_dkv_kernel": 8,  # S, dP recomputed; dV = P^T dO, dK = dS^T Q
+    # the backward (D <= 64): dQ tasks and dK/dV tasks in one launch
+    "attn_bwd_kernel": 14,
+    # the same kernel launched with one kind of task only (diagnostic split)
+    "attn_bwd_kernel[dq]": 6,   # S, dP recomputed; dQ = dS K
+    "attn_bwd_kernel[dkv]": 8,  # S, dP recomputed; dV = P^T dO, dK = dS^T Q
 }
 
 
@@ -225,8 +228,11 @@ def time_ops(pkg, iters=20):
 def time_kernels(pkg, cfg, iters):
     """Average duration of each main kernel (HIP events the library records
     around it on its launch stream, one pair per launch) and of each whole
-    stage: the forward stage adds the K-RoPE pass, the dK/dV stage the
-    partial-sum combine pass."""
+    stage: the forward stage adds the K-RoPE pass, the backward stage the
+    delta prep pass (and the partial-sum combine pass when the dK/dV heads
+    are split).  The backward kernel is also timed with only its dQ tasks
+    and only its dK/dV tasks (the library's two half-backward entry points),
+    as a diagnostic of how the two kinds share the launch."""
     native = pkg._native
     lib = native.load()
     b, t, hq, hkv, d = cfg
@@ -255,8 +261,9 @@ def time_kernels(pkg, cfg, iters):
                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
                         b, hq, hkv, t, d, s_bwd, scale, 0, cos.data_ptr(), sin.data_ptr(), sp), "bwd")
 
-    stages = [("attn_fwd_kernel", fwd), ("attn_bwd_dq_kernel", lambda: bwd(lib.mt_gqa_attn_bwd_dq)),
-              ("attn_bwd_dkv_kernel", lambda: bwd(lib.mt_gqa_attn_bwd_dkv))]
+    stages = [("attn_fwd_kernel", fwd), ("attn_bwd_kernel", lambda: bwd(lib.mt_gqa_attn_bwd)),
+              ("attn_bwd_kernel[dq]", lambda: bwd(lib.mt_gqa_attn_bwd_dq)),
+              ("attn_bwd_kernel[dkv]", lambda: bwd(lib.mt_gqa_attn_bwd_dkv))]
     for _ in range(3):
         for _, fn in stages:
             fn()
@@ -601,7 +608,7 @@ def main(argv=None) -> int:
     value = flops / (ms_event * 1e-3) / 1e12
 
     kern = time_kernels(pkg, C3, max(10, args.steps // 2))
-    dom = max(kern, key=lambda n: kern[n]["ms"])
+    dom = max((n for n in kern if "[" not in n), key=lambda n: kern[n]["ms"])
     achieved = kern[dom]["tflops"]
 
     ms_c2, _ = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)

@@ -50,6 +50,9 @@ def compile_command(out: str = LIB_PATH, sources: list[str] | None = None) -> li
         # never let the compiler form packed-fp32 ALU ops (v_pk_{add,mul,fma}_f32)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-pass-failed",
+        # one soname for every build, so the attention ops library binds to
+        # whichever libmt_attn.so the process loaded first
+        "-Wl,-soname," + os.path.basename(LIB_PATH if sources is None else out).replace(".tmp", ""),
         "-o", out,
         *[os.path.join(CSRC, s) for s in (SOURCES if sources is None else sources)],
     ]

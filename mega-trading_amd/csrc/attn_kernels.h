@@ -67,6 +67,8 @@ struct AttnParams {
   int nsb;        // ceil(nqb / rb)
   int n_split;    // dK/dV: workgroups sharing one key block (split of the R heads)
   int nkb;        // dK/dV: key blocks
+  int n_kv_tasks; // attn_bwd_kernel: dK/dV workgroups in the grid
+  int n_dq_tasks; // attn_bwd_kernel: dQ workgroups in the grid
   float scale;       // softmax scale (1/sqrt(D) by default)
   float scale_log2;  // scale * log2(e)
 };
@@ -115,9 +117,8 @@ __device__ __forceinline__ void rope_back4(float& x0, float& x1, float& x2, floa
 struct RowTask {
   int b, kvh, hs, sb;
 };
-__device__ __forceinline__ RowTask row_task(const AttnParams& p) {
+__device__ __forceinline__ RowTask row_task(const AttnParams& p, int L) {
   const int groups = p.B * p.Hkv * p.n_hsub;
-  const int L = blockIdx.x;
   RowTask t;
   t.sb = p.nsb - 1 - L / groups;
   const int g = L % groups;
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
   // [buf][K, V] x 128 rows (two 64-row tiles back to back)
   __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];
 
-  const RowTask task = row_task(p);
+  const RowTask task = row_task(p, blockIdx.x);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -567,7 +568,7 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
   constexpr int SW = TL::INSTR < kFwdW8Waves ? TL::INSTR : kFwdW8Waves;  // waves that stage tiles
   __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];  // [buf][K, V] x 128 rows
 
-  const RowTask task = row_task(p);
+  const RowTask task = row_task(p, blockIdx.x);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -766,21 +767,30 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
   }
 }
 
-// PEEL: the workgroup's 4 waves are 4 heads of one row block, so every active
-// wave's diagonal tile is the workgroup's last tile and is handled after the
-// loop; keeping the masked tile out of the loop keeps the loop within the
-// register budget.
+// LDS of one dQ workgroup (D <= 64): double-buffered K / V tiles, then the
+// 4 waves' offset blocks.
+template <int D>
+struct DqLds {
+  static constexpr int TILES = 2 * 2 * Tile<D>::BYTES;          // [buf][K, V]
+  static constexpr int BYTES = TILES + 4 * kDqOffsFloats * 4;
+};
+
+// One dQ workgroup (task L of the dQ grid).  PEEL: the workgroup's 4 waves
+// are 4 heads of one row block, so every active wave's diagonal tile is the
+// workgroup's last tile and is handled after the loop; keeping the masked
+// tile out of the loop keeps the loop within the register budget.  The rows'
+// -delta and -LSE log2(e) come from attn_bwd_prep_kernel.
 template <class E, int D, bool ROPE, bool PEEL>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
+__device__ __forceinline__ void dq_body(const AttnParams& p, int L, char* lds) {
   static_assert(D <= 64, "D = 128 uses attn_bwd_dq_w8_kernel");
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
-  __shared__ __attribute__((aligned(16))) float offs_all[4][kDqOffsFloats];
+  char (*smem)[2][TL::BYTES] = reinterpret_cast<char (*)[2][TL::BYTES]>(lds);  // [buf][K, V]
+  float (*offs_all)[kDqOffsFloats] = reinterpret_cast<float (*)[kDqOffsFloats]>(lds + DqLds<D>::TILES);
 
-  const RowTask task = row_task(p);
+  const RowTask task = row_task(p, L);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -801,11 +811,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
   {
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     const uint16_t* gbase = p.dout + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
-    const uint16_t* obase = p.o + task.b * p.so[0] + (int64_t)head * p.so[1];
     // all loads first (one memory round trip; rows past T load row T-1 and
-    // are zeroed), then delta and the stores
-    u32x4 qx[2][KT], gx[2][KT], ox[2][KT];
-    float lx[2];
+    // are zeroed), then the operands and the offset block
+    u32x4 qx[2][KT], gx[2][KT];
+    float nlx[2], ndx[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int rc = min(q0 + nt * 32 + l32, p.T - 1);
@@ -814,16 +823,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
         const int d0 = 16 * kk + 8 * hh;
         qx[nt][kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
         gx[nt][kk] = *reinterpret_cast<const u32x4*>(gbase + (int64_t)rc * p.sdo[2] + d0);
-        ox[nt][kk] = *reinterpret_cast<const u32x4*>(obase + (int64_t)rc * p.so[2] + d0);
       }
-      lx[nt] = p.lse[rowbase + rc];
+      nlx[nt] = p.nlse2[rowbase + rc];
+      ndx[nt] = p.ndelta[rowbase + rc];
     }
     const float c2 = p.scale_log2;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int row = q0 + nt * 32 + l32;
       const bool ok = active && row < p.T;
-      float dsum = 0.f;
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
         // Q pre-multiplied by scale * log2(e) (rounded to the storage type once,
@@ -832,21 +840,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnParams p) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) qs[w] = pack2<E>(lo_f<E>(qs[w]) * c2, hi_f<E>(qs[w]) * c2);
         qop[nt][kk] = __builtin_bit_cast(V8, qs);
-        const u32x4 g = ok ? gx[nt][kk] : zero4();
-        const u32x4 o = ox[nt][kk];
-        gop[nt][kk] = __builtin_bit_cast(V8, g);
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          dsum += lo_f<E>(g[w]) * lo_f<E>(o[w]) + hi_f<E>(g[w]) * hi_f<E>(o[w]);
+        gop[nt][kk] = __builtin_bit_cast(V8, ok ? gx[nt][kk] : zero4());
       }
-      dsum = sum_with_partner(dsum);
-      const float lse2 = ok ? lx[nt] * kLog2e : 0.f;
-      if (ok && hh == 0) {  // negated: the dK/dV pass seeds its accumulators with them
-        p.ndelta[rowbase + row] = -dsum;
-        p.nlse2[rowbase + row] = -lse2;
-      }
+      const float nlse2 = ok ? nlx[nt] : 0.f;
+      const float ndelta = ok ? ndx[nt] : 0.f;
       // this wave's offset block: lanes hh = 0 / 1 fill groups 0-1 / 2-3
-      const f32x4 nl = {-lse2, -lse2, -lse2, -lse2}, nd = {-dsum, -dsum, -dsum, -dsum};
+      const f32x4 nl = {nlse2, nlse2, nlse2, nlse2}, nd = {ndelta, ndelta, ndelta, ndelta};
 #pragma unroll
       for (int g = 2 * hh; g < 2 * hh + 2; ++g) {
         *reinterpret_cast<f32x4*>(offs + (0 * 2 + nt) * 512 + g * 128 + l32 * 4) = nl;
@@ -975,7 +974,7 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_bwd_dq_w8_kernel(Att
   constexpr int SW = TL::INSTR < kFwdW8Waves ? TL::INSTR : kFwdW8Waves;  // waves that stage tiles
   __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
 
-  const RowTask task = row_task(p);
+  const RowTask task = row_task(p, blockIdx.x);
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -994,40 +993,28 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_bwd_dq_w8_kernel(Att
   const int64_t rowbase = ((int64_t)task.b * p.Hq + head) * p.T;
 
   V8 qop[KT], gop[KT];
-  float lse2, dlt;
+  float lse2, dlt;  // LSE log2(e) and delta of the lane's row (from attn_bwd_prep_kernel)
   {
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     const uint16_t* gbase = p.dout + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
-    const uint16_t* obase = p.o + task.b * p.so[0] + (int64_t)head * p.so[1];
     const int row = q0 + l32;
     const int rc = min(row, p.T - 1);
     const bool ok = active && row < p.T;
-    u32x4 qx[KT], gx[KT], ox[KT];
+    u32x4 qx[KT], gx[KT];
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
       const int d0 = 16 * kk + 8 * hh;
       qx[kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
       gx[kk] = *reinterpret_cast<const u32x4*>(gbase + (int64_t)rc * p.sdo[2] + d0);
-      ox[kk] = *reinterpret_cast<const u32x4*>(obase + (int64_t)rc * p.so[2] + d0);
     }
-    const float lx = p.lse[rowbase + rc];
-    float dsum = 0.f;
+    const float nl = p.nlse2[rowbase + rc], nd = p.ndelta[rowbase + rc];
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
       qop[kk] = __builtin_bit_cast(V8, ok ? qx[kk] : zero4());
-      const u32x4 g = ok ? gx[kk] : zero4();
-      const u32x4 o = ox[kk];
-      gop[kk] = __builtin_bit_cast(V8, g);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) dsum += lo_f<E>(g[w]) * lo_f<E>(o[w]) + hi_f<E>(g[w]) * hi_f<E>(o[w]);
+      gop[kk] = __builtin_bit_cast(V8, ok ? gx[kk] : zero4());
     }
-    dsum = sum_with_partner(dsum);
-    dlt = dsum;
-    lse2 = ok ? lx * kLog2e : 0.f;
-    if (ok && hh == 0) {  // negated: the dK/dV pass seeds its accumulators with them
-      p.ndelta[rowbase + row] = -dsum;
-      p.nlse2[rowbase + row] = -lse2;
-    }
+    dlt = ok ? -nd : 0.f;
+    lse2 = ok ? -nl : 0.f;
   }
 
   f32x16 dqacc[DT];
@@ -1262,19 +1249,26 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
   (void)NS;
 }
 
+// LDS of one dK/dV workgroup: [buf][Q, dO] x 128 rows (two 64-row tiles back
+// to back), then [buf][-lse * log2(e), -delta] of those rows.
+template <int D>
+struct DkvLds {
+  static constexpr int TILES = 2 * 2 * 2 * Tile<D>::BYTES;
+  static constexpr int BYTES = TILES + 2 * 2 * kKvRows * 4;
+};
+
+// One dK/dV workgroup (task L of the dK/dV grid).
 template <class E, int D, bool ROPE>
-__global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_kernel(AttnParams p) {
+__device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  // [buf][Q, dO] x 128 rows (two 64-row tiles back to back)
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];
-  __shared__ __attribute__((aligned(16))) float vec[2][2][kKvRows];  // [buf][-lse * log2(e), -delta]
+  char (*smem)[2][2 * TL::BYTES] = reinterpret_cast<char (*)[2][2 * TL::BYTES]>(lds);
+  float (*vec)[2][kKvRows] = reinterpret_cast<float (*)[2][kKvRows]>(lds + DkvLds<D>::TILES);
 
   // heaviest key blocks (smallest index: most causal rows) first
   const int groups = p.B * p.Hkv * p.n_split;
-  const int L = blockIdx.x;
   const int kb = L / groups;
   const int g = L % groups;
   const int hs = g % p.n_split;
@@ -1406,6 +1400,73 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
         *reinterpret_cast<f32x4*>(pk + d) = xk;
         *reinterpret_cast<f32x4*>(pv + d) = xv;
       }
+  }
+}
+
+template <class E, int D, bool ROPE>
+__global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(1024))) char lds[DkvLds<D>::BYTES];
+  dkv_body<E, D, ROPE>(p, blockIdx.x, lds);
+}
+
+// ===========================================================================
+// Backward, dQ and dK/dV work in one launch (D <= 64)
+// ===========================================================================
+// The n_kv dK/dV tasks and the n_dq dQ tasks are independent once the prep
+// pass has written -delta and -LSE log2(e), so one grid holds both: block L
+// is a dK/dV task when the proportional interleave floor(L n_kv / N) steps
+// at L, else a dQ task.  Both task lists are heaviest first, so the merged
+// order is close to heaviest first overall and the light tasks of either kind
+// fill the slots the other kind's long tasks leave at the end.
+template <int D>
+struct BwdLds {
+  static constexpr int BYTES = DqLds<D>::BYTES > DkvLds<D>::BYTES ? DqLds<D>::BYTES : DkvLds<D>::BYTES;
+};
+
+template <class E, int D, bool ROPE, bool PEEL>
+__global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnParams p) {
+  static_assert(kKvWaves == 4, "dQ and dK/dV workgroups must have the same size");
+  __shared__ __attribute__((aligned(1024))) char lds[BwdLds<D>::BYTES];
+  const int L = blockIdx.x;
+  const int n = p.n_kv_tasks + p.n_dq_tasks;
+  const int kv_before = (int)((int64_t)L * p.n_kv_tasks / n);
+  const int kv_through = (int)((int64_t)(L + 1) * p.n_kv_tasks / n);
+  if (kv_through > kv_before)
+    dkv_body<E, D, ROPE>(p, kv_before, lds);
+  else
+    dq_body<E, D, ROPE, PEEL>(p, L - kv_before, lds);
+}
+
+// ===========================================================================
+// Backward prep: -delta = -rowsum(O * dO) and -LSE log2(e) per query row
+// ===========================================================================
+// delta is computed in fp32 from the 16-bit O and dO (triton_attention.py:561);
+// both vectors are stored negated because the dQ and dK/dV passes seed their
+// score and dP accumulators with them.  D/8 lanes per row, each summing one
+// 16-byte chunk, then a butterfly over those lanes.
+template <class E, int D>
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(AttnParams p) {
+  constexpr int LPR = D / 8;  // lanes per row
+  const int64_t rows = (int64_t)p.B * p.Hq * p.T;
+  const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  const int c = threadIdx.x % LPR;
+  float sum = 0.f;
+  if (row < rows) {
+    const int t = int(row % p.T);
+    const int64_t bh = row / p.T;
+    const int h = int(bh % p.Hq);
+    const int64_t b = bh / p.Hq;
+    const u32x4 o = *reinterpret_cast<const u32x4*>(p.o + b * p.so[0] + h * p.so[1] + (int64_t)t * p.so[2] + 8 * c);
+    const u32x4 g =
+        *reinterpret_cast<const u32x4*>(p.dout + b * p.sdo[0] + h * p.sdo[1] + (int64_t)t * p.sdo[2] + 8 * c);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sum += lo_f<E>(g[w]) * lo_f<E>(o[w]) + hi_f<E>(g[w]) * hi_f<E>(o[w]);
+  }
+#pragma unroll
+  for (int m = 1; m < LPR; m <<= 1) sum += __shfl_xor(sum, m, LPR);
+  if (c == 0 && row < rows) {
+    p.ndelta[row] = -sum;
+    p.nlse2[row] = -p.lse[row] * kLog2e;
   }
 }
 

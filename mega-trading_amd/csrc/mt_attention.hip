@@ -97,17 +97,25 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, const float* c
 
 int kv_keys(int) { return mt::kKvKeys; }
 
-// How many workgroups share a key block in the dK/dV pass: the smallest
-// divisor of R that gives about four workgroups per CU (two resident per CU,
-// so two rounds), letting the heaviest-first order pair long and short
-// causal tasks.
+// How many workgroups share a key block in the dK/dV pass (each then sums a
+// subset of the group's heads into fp32 partials that a combine pass adds).
+// The smallest divisor of R that gives enough dK/dV workgroups:
+//  * D <= 64: dQ and dK/dV tasks share one grid (attn_bwd_kernel), where the
+//    many dQ tasks balance the long causal dK/dV tasks; one dK/dV task per CU
+//    suffices, and splitting further only adds the combine pass (measured:
+//    C2 and C3 are fastest unsplit).
+//  * D = 128: dK/dV runs alone; about four workgroups per CU (two resident,
+//    so two rounds) let the heaviest-first order pair long and short tasks.
+#ifndef MT_DKV_MAX_SPLIT
+#define MT_DKV_MAX_SPLIT 64
+#endif
 int choose_split(int B, int Hq, int Hkv, int T, int D) {
   const int R = Hq / Hkv;
   const int nkb = (T + kv_keys(D) - 1) / kv_keys(D);
   const long tasks = (long)nkb * B * Hkv;
-  const long want = 4L * device_cus();
+  const long want = (D <= 64 ? 1L : 4L) * device_cus();
   int split = 1;
-  for (int s = 1; s <= R; ++s) {
+  for (int s = 1; s <= R && s <= MT_DKV_MAX_SPLIT; ++s) {
     if (R % s) continue;
     split = s;
     if (tasks * s >= want) break;
@@ -177,26 +185,40 @@ hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
   }
 }
 
-// stage: 1 = dQ (+ delta), 2 = dK/dV, 3 = both
+// stage: 1 = prep (delta, LSE log2 e) + dQ, 2 = dK/dV (reads the prep vectors), 3 = all
 template <class E, int D, bool ROPE>
 hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
+  const int n_dq = p.nsb * p.B * p.Hkv * p.n_hsub;
+  const int n_kv = p.nkb * p.B * p.Hkv * p.n_split;
   if (stage & 1) {
-    dim3 grid_dq(p.nsb * p.B * p.Hkv * p.n_hsub);
-    hipError_t e;
-    if constexpr (D > 64) {
-      const dim3 block(64 * mt::kFwdW8Waves);
-      e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, true>, grid_dq, block, st, p)
-                    : launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, false>, grid_dq, block, st, p);
-    } else {
-      e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE, true>, grid_dq, dim3(256), st, p)
-                    : launch_main(mt::attn_bwd_dq_kernel<E, D, ROPE, false>, grid_dq, dim3(256), st, p);
-    }
+    const int64_t rows = (int64_t)p.B * p.Hq * p.T;
+    const int64_t rows_per_block = 256 / (D / 8);
+    hipLaunchKernelGGL((mt::attn_bwd_prep_kernel<E, D>), dim3((unsigned)((rows + rows_per_block - 1) / rows_per_block)),
+                       dim3(256), 0, st, p);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (stage & 2) {
-    dim3 grid_kv(p.nkb * p.B * p.Hkv * p.n_split);
-    hipError_t e = launch_main(mt::attn_bwd_dkv_kernel<E, D, ROPE>, grid_kv, dim3(64 * mt::kKvWaves), st, p);
+  if constexpr (D <= 64) {
+    // dQ and dK/dV tasks in one grid
+    p.n_dq_tasks = (stage & 1) ? n_dq : 0;
+    p.n_kv_tasks = (stage & 2) ? n_kv : 0;
+    const dim3 grid(p.n_dq_tasks + p.n_kv_tasks);
+    hipError_t e = p.rb == 1 ? launch_main(mt::attn_bwd_kernel<E, D, ROPE, true>, grid, dim3(256), st, p)
+                             : launch_main(mt::attn_bwd_kernel<E, D, ROPE, false>, grid, dim3(256), st, p);
     if (e != hipSuccess) return e;
+  } else {
+    if (stage & 1) {
+      const dim3 block(64 * mt::kFwdW8Waves);
+      hipError_t e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, true>, dim3(n_dq), block, st, p)
+                               : launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, false>, dim3(n_dq), block, st, p);
+      if (e != hipSuccess) return e;
+    }
+    if (stage & 2) {
+      hipError_t e = launch_main(mt::attn_bwd_dkv_kernel<E, D, ROPE>, dim3(n_kv), dim3(64 * mt::kKvWaves), st, p);
+      if (e != hipSuccess) return e;
+    }
+  }
+  if (stage & 2) {
     if (p.n_split > 1) {
       const int64_t n4 = (int64_t)p.B * p.Hkv * p.T * (D / 4);
       hipLaunchKernelGGL((mt::attn_bwd_combine_kernel<E, D, ROPE>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, p);
