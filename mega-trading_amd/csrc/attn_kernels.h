@@ -65,7 +65,7 @@ struct AttnParams {
   int rb;         // row blocks per workgroup (4 / r_sub)
   int nqb;        // ceil(T / 64)
   int nsb;        // ceil(nqb / rb)
-  int n_split;    // dK/dV: workgroups sharing one key block (split of the R heads)
+  int n_split;    // dK/dV: workgroups sharing one key block (each sums a range of the R heads)
   int nkb;        // dK/dV: key blocks
   int n_kv_tasks; // attn_bwd_kernel: dK/dV workgroups in the grid
   int n_dq_tasks; // attn_bwd_kernel: dQ workgroups in the grid
@@ -707,10 +707,13 @@ __device__ __forceinline__ f32x16 dq_offset_tile(const float* offs, int kind, in
   return r;
 }
 
+// With MASK, qoff = (the wave's row block - the tile) * 64 >= 0: keys above
+// the query are masked (only on the wave's diagonal tile, qoff = 0, does
+// anything get masked; a masked tile left of it computes as an unmasked one).
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typename E::v8 (*qop)[D / 16],
                                         const typename E::v8 (*gop)[D / 16], f32x16 (*dqacc)[2], const float* offs,
-                                        int rbase, TrBase tbase, int l32, int hh) {
+                                        int rbase, TrBase tbase, int l32, int hh, int qoff = 0) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
@@ -746,7 +749,7 @@ __device__ __forceinline__ void dq_tile(const char* K, const char* Vr, const typ
         float pv = exp2_fast(st[nt][i]);
         if constexpr (MASK) {
           const int kr = mt * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (kr > nt * 32 + l32) pv = 0.f;
+          if (kr > qoff + nt * 32 + l32) pv = 0.f;
         }
         st[nt][i] = pv * dpt[nt][i];
       }
@@ -871,23 +874,37 @@ __device__ __forceinline__ void dq_body(const AttnParams& p, int L, char* lds) {
   wait_vmem();
   __syncthreads();
 
-  for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
+  // Tiles before the workgroup's first row block are below every wave's
+  // diagonal (unmasked loop); the rb tiles from there on hold the waves'
+  // diagonals and run the masked variant (with PEEL that is the last tile).
+  const int jdiag = task.sb * p.rb;
+  for (int j = 0; j < jdiag; ++j) {
     const int buf = j & 1;
-    if (j < jlast) {
-      ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
-      vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
-    }
-    if (active && j <= qb) {
-      if (PEEL || j < qb)
-        dq_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
-      else
-        dq_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
-    }
+    ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
+    vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
+    if (active)
+      dq_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
     wait_vmem();
     __syncthreads();
   }
-  if (PEEL && active)  // qb == jlast
-    dq_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh);
+  if constexpr (PEEL) {
+    if (active)  // qb == jdiag == jlast
+      dq_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32,
+                          hh);
+  } else {
+    for (int j = jdiag; j <= jlast; ++j) {
+      const int buf = j & 1;
+      if (j < jlast) {
+        ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
+        vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
+      }
+      if (active && j <= qb)
+        dq_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, offs, rbase_op, tbase_op, l32, hh,
+                            (qb - j) * kBlk);
+      wait_vmem();
+      __syncthreads();
+    }
+  }
 
   if (!active) return;
   uint16_t* dqbase = p.out + task.b * p.sout[0] + (int64_t)head * p.sout[1];
@@ -1036,26 +1053,34 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_bwd_dq_w8_kernel(Att
   __syncthreads();
 
   const float c2 = p.scale_log2;
-  for (int j = 0; j < (PEEL ? jlast : jlast + 1); ++j) {
+  // unmasked tiles below every wave's diagonal, then the rb diagonal-zone
+  // tiles with the masked variant (row offset from the tile: a tile left of
+  // the wave's diagonal masks nothing)
+  const int jdiag = task.sb * p.rb;
+  for (int j = 0; j < jdiag; ++j) {
+    const int buf = j & 1;
+    if (stager) {
+      ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
+      vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
+    }
+    if (active)
+      dq32_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh,
+                             qoff, c2);
+    wait_vmem();
+    __syncthreads();
+  }
+  for (int j = jdiag; j <= jlast; ++j) {
     const int buf = j & 1;
     if (j < jlast && stager) {
       ks_stage.stage(smem[buf ^ 1][0], kbase, p.sk[2], (j + 1) * kBlk, p.T);
       vs_stage.stage(smem[buf ^ 1][1], vbase, p.sv[2], (j + 1) * kBlk, p.T);
     }
-    if (active && j <= qb) {
-      if (PEEL || j < qb)
-        dq32_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh,
-                               qoff, c2);
-      else
-        dq32_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh,
-                              qoff, c2);
-    }
+    if (active && j <= qb)
+      dq32_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op, l32, hh,
+                            qoff + (qb - j) * kBlk, c2);
     wait_vmem();
     __syncthreads();
   }
-  if (PEEL && active)  // qb == jlast
-    dq32_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, gop, dqacc, lse2, dlt, rbase_op, tbase_op,
-                          l32, hh, qoff, c2);
 
   if (!active) return;
   const int row = q0 + l32;
@@ -1312,7 +1337,10 @@ __device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) 
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) { zero16(dkacc[dt]); zero16(dvacc[dt]); }
 
-  const int hpt = p.R / p.n_split;                 // heads per task
+  // this task's heads: [R hs / n_split, R (hs + 1) / n_split) of the group
+  // (uneven when n_split does not divide R)
+  const int h_lo = (p.R * hs) / p.n_split;
+  const int hpt = (p.R * (hs + 1)) / p.n_split - h_lo;  // heads per task
   const int qr0 = kb * kKvKeys;                    // first row touching these keys (128-aligned)
   const int nstep_h = (p.T - qr0 + kKvRows - 1) / kKvRows;  // 128-row steps per head
   const int n_it = hpt * nstep_h;
@@ -1338,7 +1366,7 @@ __device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) 
     stage_vec64(reinterpret_cast<char*>(&vec[buf][wave >> 1][(wave & 1) * kBlk]), src, row0 + (wave & 1) * kBlk, p.T, lane);
   };
 
-  int cur_row = qr0, nxt_head = kvh * p.R + hs * hpt, nxt_row = qr0;
+  int cur_row = qr0, nxt_head = kvh * p.R + h_lo, nxt_row = qr0;
   stage(nxt_head, nxt_row, 0);
   wait_vmem();
   __syncthreads();

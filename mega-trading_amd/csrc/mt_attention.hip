@@ -98,24 +98,33 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, const float* c
 int kv_keys(int) { return mt::kKvKeys; }
 
 // How many workgroups share a key block in the dK/dV pass (each then sums a
-// subset of the group's heads into fp32 partials that a combine pass adds).
-// The smallest divisor of R that gives enough dK/dV workgroups:
+// range of the group's heads into fp32 partials that a combine pass adds).
 //  * D <= 64: dQ and dK/dV tasks share one grid (attn_bwd_kernel), where the
-//    many dQ tasks balance the long causal dK/dV tasks; one dK/dV task per CU
-//    suffices, and splitting further only adds the combine pass (measured:
-//    C2 and C3 are fastest unsplit).
-//  * D = 128: dK/dV runs alone; about four workgroups per CU (two resident,
-//    so two rounds) let the heaviest-first order pair long and short tasks.
-#ifndef MT_DKV_MAX_SPLIT
-#define MT_DKV_MAX_SPLIT 64
+//    many dQ tasks balance the long causal dK/dV tasks.  At most 4 heads per
+//    task (split ceil(R / 4), head ranges as even as R allows), and at least
+//    one dK/dV task per CU.  Measured at T = 4096, D = 64 (fwd+bwd TFLOP/s,
+//    split 1 / 2): R = 3: 641 / 623, R = 4: 707 / 684, R = 7: 547 / 647,
+//    R = 8: 620 / 702; BASELINE config 2 and the config 5 layer are also
+//    fastest unsplit (the combine pass costs more than the balance gains).
+//  * D = 128: dK/dV runs alone; the smallest divisor of R that gives about
+//    four workgroups per CU (two resident, so two rounds) lets the
+//    heaviest-first order pair long and short tasks.
+#ifndef MT_DKV_FORCE_SPLIT
+#define MT_DKV_FORCE_SPLIT 0
 #endif
 int choose_split(int B, int Hq, int Hkv, int T, int D) {
   const int R = Hq / Hkv;
+  if (MT_DKV_FORCE_SPLIT > 0) return MT_DKV_FORCE_SPLIT < R ? MT_DKV_FORCE_SPLIT : R;
   const int nkb = (T + kv_keys(D) - 1) / kv_keys(D);
   const long tasks = (long)nkb * B * Hkv;
-  const long want = (D <= 64 ? 1L : 4L) * device_cus();
+  if (D <= 64) {
+    int split = (R + 3) / 4;
+    while (split < R && tasks * split < device_cus()) ++split;
+    return split;
+  }
+  const long want = 4L * device_cus();
   int split = 1;
-  for (int s = 1; s <= R && s <= MT_DKV_MAX_SPLIT; ++s) {
+  for (int s = 1; s <= R; ++s) {
     if (R % s) continue;
     split = s;
     if (tasks * s >= want) break;
@@ -416,11 +425,9 @@ int mt_gqa_attn_bwd_noalloc(const void* q, const void* k, const void* v, const v
   int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
   if (rc) return rc;
   // the standard head split when its partials fit, else the largest smaller
-  // divisor of R that fits (split 1 keeps only delta and LSE)
-  const int R = Hq / Hkv;
+  // one that fits (split 1 keeps only delta and LSE)
   int split = choose_split(B, Hq, Hkv, T, D);
-  while (split > 1 && (R % split || workspace_bytes_split(B, Hq, Hkv, T, D, split) > MT_NOALLOC_SCRATCH_BYTES))
-    --split;
+  while (split > 1 && workspace_bytes_split(B, Hq, Hkv, T, D, split) > MT_NOALLOC_SCRATCH_BYTES) --split;
   const size_t need = workspace_bytes_split(B, Hq, Hkv, T, D, split);
   if (need > MT_NOALLOC_SCRATCH_BYTES)
     return fail(MT_E_WORKSPACE,
