@@ -129,6 +129,27 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True):
     return start.elapsed_time(end) / steps, wall / steps * 1e3
 
 
+# The reference's own configs use other query-heads-per-KV-head ratios R:
+# configs/default.yaml:33-34 (R = 1), configs/mac.yaml:33-34 (R = 3),
+# configs/modal.yaml:33-34 (R = 7).  Measured at C3's B, T and D with the
+# query-head count nearest 16 that R divides.
+GROUP_SIZE_CASES = {"R1": (4, 4096, 16, 16, 64), "R2": (4, 4096, 16, 8, 64), "R3": (4, 4096, 12, 4, 64),
+                    "R4": C3, "R7": (4, 4096, 14, 2, 64), "R8": (4, 4096, 16, 2, 64)}
+
+
+def time_group_sizes(pkg, steps):
+    """fwd+bwd TFLOP/s of the fused-RoPE op at each group size R (same FLOP
+    convention; the FLOPs scale with Hq) and each one's ratio to R = 4."""
+    out = {}
+    for name, cfg in GROUP_SIZE_CASES.items():
+        b, t, hq, hkv, d = cfg
+        ms, _ = time_op_steps(pkg, cfg, steps, 3, rope=True)
+        out[name] = {"Hq": hq, "Hkv": hkv, "ms": round(ms, 4), "tflops": round(fwd_bwd_flops(b, t, hq, d) / (ms * 1e-3) / 1e12, 1)}
+    for name in out:
+        out[name]["vs_R4"] = round(out[name]["tflops"] / out["R4"]["tflops"], 3)
+    return out
+
+
 def mfma_ceiling(iters=20000, repeats=3):
     """Sustained whole-GPU bf16 MFMA rate (random and zero operands) with the clock it ran at."""
     path = os.path.join(ROOT, "mega-trading_amd", "libmt_probe.so")
@@ -612,6 +633,7 @@ def main(argv=None) -> int:
     achieved = kern[dom]["tflops"]
 
     ms_c2, _ = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)
+    group_sizes = time_group_sizes(pkg, max(10, args.steps // 3))
     ms_c3_plain, _ = time_op_steps(pkg, C3, max(10, args.steps // 2), 3, rope=False)
     ms_c4, _ = time_op_steps(pkg, C4, max(10, args.steps // 4), 3, rope=True)
     ceiling = mfma_ceiling()
@@ -655,6 +677,7 @@ def main(argv=None) -> int:
             "C4_fwd_bwd_tflops": round(fwd_bwd_flops(C4[0], C4[1], C4[2], C4[4]) / (ms_c4 * 1e-3) / 1e12, 2),
             "C4_ms_per_step": round(ms_c4, 4),
             "wall_ms_per_step": round(ms_wall, 4),
+            "group_sizes": group_sizes,
         },
     }
     sdpa = sdpa_comparators(pkg, {"C2": C2, "C3": C3, "C4": C4}, steps=max(5, args.steps // 5))
