@@ -27,7 +27,11 @@
  *   - K and V have Hkv heads, Q / O / dO / dQ have Hq = Hkv * repeats heads;
  *     query head h reads KV head h / repeats (triton_attention.py:299).
  *   - Causal, top-left aligned, Tq == Tk == T, any T >= 1.
- *   - D in {32, 64, 128}; dtype MT_DTYPE_BF16 or MT_DTYPE_FP16.
+ *   - D in {32, 64, 128}; dtype MT_DTYPE_BF16 or MT_DTYPE_FP16, or MT_DTYPE_FP32
+ *     for the forward and backward (computed in full fp32 on fp32 MFMA: at
+ *     least the precision of the reference's fp32 path, whose forward dots
+ *     run in TF32 and whose backward is dense fp32, triton_attention.py:88-111).
+ *     Decode takes 16-bit caches only.
  *   - lse is fp32 [B, Hq, T] contiguous, the natural-log logsumexp of the
  *     scaled scores (triton_attention.py:346-349).
  *   - rope_cos / rope_sin: either both NULL (no RoPE) or both fp32
@@ -53,6 +57,7 @@ extern "C" {
 
 #define MT_DTYPE_BF16 0
 #define MT_DTYPE_FP16 1
+#define MT_DTYPE_FP32 2 /* attention forward / backward only; full-fp32 MFMA kernels */
 
 #define MT_OK 0
 #define MT_E_NULL (-1)      /* a required pointer is NULL */

@@ -43,9 +43,10 @@ def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, re
     ``query`` [B, Hq, T, D]; ``key``/``value`` [B, Hkv, T, D] with
     ``Hq == Hkv * repeats``; query head ``h`` attends to KV head ``h // repeats``.
     Scale ``1/sqrt(D)``, top-left causal mask.  Any strides with a unit last
-    stride are used in place.  fp32 inputs run through the bf16 kernels and
-    come back as fp32 (the reference's fp32 path likewise computes its dots at
-    reduced precision, TF32).
+    stride are used in place.  bf16 / fp16 inputs run on the 16-bit MFMA
+    kernels (fp32 accumulation and softmax); fp32 inputs run on full-fp32
+    MFMA kernels, at least as precise as the reference's fp32 path (TF32
+    forward dots, dense fp32 backward, ``triton_attention.py:88-111``).
     """
     _validate(query, key, value, repeats)
     out, _lse = _forward(query, key, value, None, None)
@@ -272,9 +273,6 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def _forward(q, k, v, cos, sin):
-    if q.dtype == torch.float32:
-        o, lse = _forward(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), cos, sin)
-        return o.to(torch.float32), lse
     _native.load()
     scale = 1.0 / math.sqrt(q.shape[-1])
     if cos is None:

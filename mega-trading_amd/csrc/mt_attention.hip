@@ -13,6 +13,7 @@
 #include <mutex>
 
 #include "../../include/mt_attention.h"
+#include "attn_f32_kernels.h"
 #include "attn_kernels.h"
 #include "decode_kernels.h"
 #include "mt_abi.h"
@@ -88,7 +89,8 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, const float* c
   if (B < 1 || Hq < 1 || Hkv < 1 || T < 1) return fail(MT_E_SHAPE, "B, Hq, Hkv and T must be >= 1 (got %d, %d, %d, %d)", B, Hq, Hkv, T);
   if (Hq % Hkv) return fail(MT_E_SHAPE, "query heads (%d) must equal key/value heads (%d) multiplied by repeats", Hq, Hkv);
   if (D != 32 && D != 64 && D != 128) return fail(MT_E_SHAPE, "head_dim %d unsupported (32, 64 or 128)", D);
-  if (dtype != MT_DTYPE_BF16 && dtype != MT_DTYPE_FP16) return fail(MT_E_DTYPE, "dtype code %d unsupported", dtype);
+  if (dtype != MT_DTYPE_BF16 && dtype != MT_DTYPE_FP16 && dtype != MT_DTYPE_FP32)
+    return fail(MT_E_DTYPE, "dtype code %d unsupported", dtype);
   if ((cs == nullptr) != (sn == nullptr)) return fail(MT_E_ROPE, "rope_cos and rope_sin must both be given or both be NULL");
   if (cs && (reinterpret_cast<uintptr_t>(cs) % 16 || reinterpret_cast<uintptr_t>(sn) % 16))
     return fail(MT_E_ROPE, "RoPE tables must be 16-byte aligned");
@@ -237,6 +239,48 @@ hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
   return hipSuccess;
 }
 
+// fp32 tensors: the fp32-MFMA kernels of attn_f32_kernels.h (K rotated by its
+// own pass with RoPE, as for 16-bit; no dK/dV head split)
+template <int D, bool ROPE>
+hipError_t launch_fwd_f32(mt::AttnParams p, hipStream_t st, int) {
+  if (ROPE) {
+    const int64_t n4 = (int64_t)p.B * p.Hkv * p.T * (D / 4);
+    hipLaunchKernelGGL((mt::rope_f32_kernel<D>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(p.k), p.sk[0], p.sk[1], p.sk[2], reinterpret_cast<float*>(p.dk),
+                       p.cos, p.sin, p.Hkv, p.T, n4);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    p.k = p.dk;
+    p.sk[0] = (int64_t)p.Hkv * p.T * D;
+    p.sk[1] = (int64_t)p.T * D;
+    p.sk[2] = D;
+  }
+  const int64_t waves = (int64_t)p.B * p.Hq * ((p.T + 31) / 32);
+  return launch_main(mt::attn_fwd_f32_kernel<D, ROPE>, dim3((unsigned)((waves + 3) / 4)), dim3(256), st, p);
+}
+
+template <int D, bool ROPE>
+hipError_t launch_bwd_f32(mt::AttnParams p, hipStream_t st, int stage) {
+  const int nblk = (p.T + 31) / 32;
+  if (stage & 1) {
+    const int64_t rows = (int64_t)p.B * p.Hq * p.T;
+    const int64_t rows_per_block = 256 / (D / 4);
+    hipLaunchKernelGGL((mt::attn_bwd_prep_f32_kernel<D>), dim3((unsigned)((rows + rows_per_block - 1) / rows_per_block)),
+                       dim3(256), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t waves = (int64_t)p.B * p.Hq * nblk;
+    e = launch_main(mt::attn_bwd_dq_f32_kernel<D, ROPE>, dim3((unsigned)((waves + 3) / 4)), dim3(256), st, p);
+    if (e != hipSuccess) return e;
+  }
+  if (stage & 2) {
+    const int64_t waves = (int64_t)p.B * p.Hkv * nblk;
+    hipError_t e = launch_main(mt::attn_bwd_dkv_f32_kernel<D, ROPE>, dim3((unsigned)((waves + 3) / 4)), dim3(256), st, p);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 using Launcher = hipError_t (*)(mt::AttnParams, hipStream_t, int);
 
 template <bool FWD, class E, int D>
@@ -245,8 +289,19 @@ Launcher pick_rope(bool rope) {
   return rope ? &launch_bwd<E, D, true> : &launch_bwd<E, D, false>;
 }
 
+template <bool FWD, int D>
+Launcher pick_f32(bool rope) {
+  if (FWD) return rope ? &launch_fwd_f32<D, true> : &launch_fwd_f32<D, false>;
+  return rope ? &launch_bwd_f32<D, true> : &launch_bwd_f32<D, false>;
+}
+
 template <bool FWD>
 Launcher pick(int dtype, int D, bool rope) {
+  if (dtype == MT_DTYPE_FP32) {
+    if (D == 32) return pick_f32<FWD, 32>(rope);
+    if (D == 64) return pick_f32<FWD, 64>(rope);
+    return pick_f32<FWD, 128>(rope);
+  }
   if (dtype == MT_DTYPE_BF16) {
     if (D == 32) return pick_rope<FWD, mt::BF16, 32>(rope);
     if (D == 64) return pick_rope<FWD, mt::BF16, 64>(rope);
@@ -461,6 +516,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
                 size_t workspace_bytes, void* stream) {
   int rc = check_common(B, Hq, Hkv, L, D, dtype, nullptr, nullptr);
   if (rc) return rc;
+  if (dtype == MT_DTYPE_FP32) return fail(MT_E_DTYPE, "decode attention takes bfloat16 or float16 caches");
   if (Hq / Hkv > mt::kDecMaxR)
     return fail(MT_E_SHAPE, "decode supports up to %d query heads per KV head (got %d)", mt::kDecMaxR, Hq / Hkv);
   if (!strides) return fail(MT_E_NULL, "strides is NULL");
@@ -524,6 +580,7 @@ int mt_decode_rope_append(const void* q, const void* k, const void* v, const int
                           int in_dtype, int dtype, void* stream) {
   int rc = check_common(B, Hq, Hkv, 1, D, dtype, rope_cos, rope_sin);
   if (rc) return rc;
+  if (dtype == MT_DTYPE_FP32) return fail(MT_E_DTYPE, "the KV caches must be bfloat16 or float16");
   if (!q || !k || !v || !q_rot || !k_cache || !v_cache || !rope_cos || !in_strides || !cache_strides)
     return fail(MT_E_NULL, "q, k, v, q_rot, k_cache, v_cache, rope tables and strides must be non-NULL");
   if (in_dtype != MT_DTYPE_BF16 && in_dtype != MT_DTYPE_FP16 && in_dtype != 2)

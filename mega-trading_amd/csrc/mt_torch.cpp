@@ -42,7 +42,8 @@ void put_strides(int64_t* dst, const at::Tensor& t) {
 int dtype_code(const at::Tensor& t) {
   if (t.scalar_type() == at::kBFloat16) return MT_DTYPE_BF16;
   if (t.scalar_type() == at::kHalf) return MT_DTYPE_FP16;
-  TORCH_CHECK(false, "hip attention kernels take bfloat16 or float16 tensors (got ", t.scalar_type(), ")");
+  if (t.scalar_type() == at::kFloat) return MT_DTYPE_FP32;
+  TORCH_CHECK(false, "hip attention kernels take bfloat16, float16 or float32 tensors (got ", t.scalar_type(), ")");
 }
 
 void check_rc(int rc, const char* what) {

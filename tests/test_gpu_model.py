@@ -138,3 +138,24 @@ def test_attention_only_train_step_runs_with_the_trainer_loss():
     print("losses", losses)
     for a, b in zip(losses["attention_only"], losses["auto"]):
         assert abs(a - b) <= TOL_LOSS_REL * abs(b)
+
+
+def test_fp32_model_without_autocast_matches_the_sdpa_route():
+    """A fp32 decoder without autocast (the reference trainer's precision "fp32":
+    no mixed precision, trainer.py:940-945,1009-1010) sends fp32 q/k/v to the
+    attention op, which computes in fp32: loss and gradients agree with the SDPA
+    route (fp32) to fp32 rounding."""
+    ids, labels = workload.zipf_batch(2, 300, SMALL["vocab_size"], seed=6)
+    ids, labels = ids.cuda(), labels.cuda()
+    out = {}
+    for route in ("auto", "triton"):
+        m = workload.build_model(route, seed=0, device="cuda", **SMALL)
+        loss, _ = m.forward_with_loss(ids, labels, return_logits=True)
+        loss.backward()
+        out[route] = (loss.detach(), {n: p.grad.detach().clone() for n, p in m.named_parameters()})
+    (l_ref, g_ref), (l_hip, g_hip) = out["auto"], out["triton"]
+    print(f"fp32 loss hip={l_hip.item():.7f} sdpa={l_ref.item():.7f}")
+    assert abs(l_hip.item() - l_ref.item()) <= 1e-5 * abs(l_ref.item())
+    worst = max(_rel(g_hip[n], g_ref[n]) for n in g_ref)
+    print(f"worst fp32 grad rel err {worst:.3e}")
+    assert worst <= 1e-4
