@@ -135,7 +135,10 @@ int mt_swiglu_packed_bwd(const void* gu, const void* dout, void* dgu, int64_t ro
  * with *n_valid (device int64) the number of labels != ignore_index; rows labelled
  * ignore_index give 0.  With write_grad != 0 the logits are overwritten in place by
  * (softmax(row) - onehot(label)) / n_valid (zero rows for ignored labels).  A label
- * outside [0, vocab) gives a NaN loss.  vocab % 8 == 0; rows 16-byte aligned. */
+ * outside [0, vocab) gives a NaN loss.  Any vocab >= 1; row_stride is a multiple
+ * of 8 and at least vocab rounded up to 8: when vocab % 8 != 0 the columns
+ * [vocab, row_stride) of each row are read as padding (ignored) and, with
+ * write_grad, overwritten with 0.  Rows 16-byte aligned. */
 int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* labels, int64_t rows, int vocab,
                           const int64_t* n_valid, int64_t ignore_index, float* loss_rows, int write_grad, int dtype,
                           void* stream);

@@ -447,13 +447,14 @@ int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* label
   int rc;
   if ((rc = check_dtype(dtype, dtype))) return rc;
   if (rows < 0 || rows > 0x7fffffffLL) return fail(MT_E_SHAPE, "rows must be in [0, 2^31) (got %lld)", (long long)rows);
-  if (vocab < 8 || vocab % 8) return fail(MT_E_SHAPE, "vocab %d unsupported (a positive multiple of 8)", vocab);
+  if (vocab < 1) return fail(MT_E_SHAPE, "vocab %d unsupported (positive)", vocab);
   if (rows == 0) return ok();
-  if ((rc = check_ptr("logits", logits)) || (rc = check_stride("logits", row_stride, vocab))) return rc;
+  // the row's last 8-value chunk may reach into the padding up to vocab rounded up to 8
+  if ((rc = check_ptr("logits", logits)) || (rc = check_stride("logits", row_stride, (vocab + 7) / 8 * 8))) return rc;
   if (!labels || !n_valid || !loss_rows) return fail(MT_E_NULL, "labels, n_valid and loss_rows must be non-NULL");
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)rows);
-  const int nch = (vocab / 8 + 255) / 256;  // 8-value chunks per thread
+  const int nch = ((vocab + 7) / 8 + 255) / 256;  // 8-value chunks per thread
   if (dtype == MT_DTYPE_BF16) ce_dispatch<K::kDtBF16>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
   else if (dtype == MT_DTYPE_FP16) ce_dispatch<K::kDtFP16>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
   else ce_dispatch<K::kDtFP32>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);

@@ -436,6 +436,9 @@ __global__ __launch_bounds__(256) void swiglu_packed_bwd_kernel(const void* gu, 
 // Rows whose label is ignore_index get loss 0 and (GRAD) a zero row.  n_valid is
 // read from device memory (no host synchronisation); n_valid = 0 gives zeros.  A
 // label outside [0, V) gives a NaN loss (the row is still read in bounds).
+// When V is not a multiple of 8 the row's last chunk reaches into the row's
+// padding (the row stride is at least V rounded up to 8): those columns count
+// as -inf in pass 1 and are written 0 in pass 2.
 // ===========================================================================
 struct MaxSum {
   float m, s;
@@ -446,6 +449,13 @@ __device__ __forceinline__ MaxSum ms_combine(MaxSum a, MaxSum b) {
   if (b.m == -INFINITY) return a;
   const float m = fmaxf(a.m, b.m);
   return MaxSum{m, a.s * __expf(a.m - m) + b.s * __expf(b.m - m)};
+}
+
+// columns j >= n of a chunk of 8 are padding: -inf (no contribution)
+__device__ __forceinline__ void mask_tail(float* v, int n) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j >= n) v[j] = -INFINITY;
 }
 
 __device__ __forceinline__ MaxSum chunk_max_sum(const float* v) {
@@ -465,7 +475,8 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t base = row * ld;
-  const int nvec = V >> 3;
+  const int nvec = (V + 7) >> 3;
+  const int tail = V - 8 * (nvec - 1);  // real columns of the last chunk (1..8)
   const int64_t label = labels[row];
   const int64_t nv = *n_valid;
   const float inv_n = nv > 0 ? 1.f / float(nv) : 0.f;
@@ -483,7 +494,10 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
       const int c = tid + 256 * k;
-      if (c < nvec) IO<DT>::load8(logits, base + 8 * c, v[k]);
+      if (c < nvec) {
+        IO<DT>::load8(logits, base + 8 * c, v[k]);
+        if (c == nvec - 1) mask_tail(v[k], tail);
+      }
     }
 #pragma unroll
     for (int k = 0; k < NCH; ++k)
@@ -491,6 +505,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
   } else {
     for (int c = tid; c < nvec; c += 256) {
       IO<DT>::load8(logits, base + 8 * c, v[0]);
+      if (c == nvec - 1) mask_tail(v[0], tail);
       acc = ms_combine(acc, chunk_max_sum(v[0]));
     }
   }
@@ -513,7 +528,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
     auto grad8 = [&](int c, float* x) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float p = __expf(x[j] - lse);
+        const float p = __expf(x[j] - lse);  // 0 for the -inf padding
         x[j] = (p - (8 * c + j == label ? 1.f : 0.f)) * inv_n;
       }
       IO<DT>::store8(logits, base + 8 * c, x);
@@ -527,6 +542,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
     } else {
       for (int c = tid; c < nvec; c += 256) {
         IO<DT>::load8(logits, base + 8 * c, v[0]);
+        if (c == nvec - 1) mask_tail(v[0], tail);
         grad8(c, v[0]);
       }
     }

@@ -136,8 +136,6 @@ def fused_linear_cross_entropy(
         raise ValueError("labels must be an integer tensor")
     _check_device_dtype(hidden, "hidden")
     _check_device_dtype(weight, "weight")
-    if weight.shape[0] % 8:
-        raise ValueError(f"vocab size {weight.shape[0]} unsupported: a multiple of 8")
     if torch.is_autocast_enabled("cuda"):
         compute = torch.get_autocast_dtype("cuda")
     else:
@@ -484,15 +482,24 @@ def fused_linear_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Te
     ct = _DTYPE_OF[compute_dtype]
     rows, h = hidden.shape
     vocab = weight.shape[0]
+    # a vocab that is not a multiple of 8 (the reference tokenizer's always is
+    # odd) gets zero weight rows up to the next multiple: the logits rows then
+    # have a padded stride, and the row kernel ignores the pad columns and
+    # writes them a zero gradient, so the pad rows contribute nothing
+    vpad = (vocab + 7) // 8 * 8
     hc = hidden.to(ct).contiguous()
-    wc = weight.to(ct).contiguous()
+    if vpad == vocab:
+        wc = weight.to(ct).contiguous()
+    else:
+        wc = torch.zeros((vpad, h), device=weight.device, dtype=ct)
+        wc[:vocab].copy_(weight)
     lab = labels.to(torch.int64).contiguous()
     n_valid = (lab != ignore_index).sum()  # stays on the device: the kernel reads it
     loss_rows = torch.empty((rows,), device=hidden.device, dtype=torch.float32)
     if need_grad:
         gh = torch.empty((rows, h), device=hidden.device, dtype=ct)
-        gw = torch.zeros((vocab, h), device=hidden.device, dtype=torch.float32)
-    chunk = max(1, min(rows, _CE_CHUNK_BYTES // (vocab * ct.itemsize)))
+        gw = torch.zeros((vpad, h), device=hidden.device, dtype=torch.float32)
+    chunk = max(1, min(rows, _CE_CHUNK_BYTES // (vpad * ct.itemsize)))
     with torch.cuda.device(hidden.device), tuned_gemms():
         stream = _stream(hidden)
         for start in range(0, rows, chunk):
@@ -508,7 +515,7 @@ def fused_linear_ce(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Te
     loss = loss_rows.sum()
     if not need_grad:
         return loss, hidden.new_empty((0,)), weight.new_empty((0,))
-    return loss, gh.to(hidden.dtype), gw.to(weight.dtype)
+    return loss, gh.to(hidden.dtype), gw[:vocab].to(weight.dtype)
 
 
 @fused_linear_ce.register_fake

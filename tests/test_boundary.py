@@ -95,7 +95,9 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     assert lib.mt_swiglu_fwd(p, p + 8, p, 100, BF16, None) == -3
     assert lib.mt_swiglu_bwd(p, p, None, p, p, 100, BF16, None) == -1
     assert lib.mt_swiglu_fwd(None, None, None, 0, BF16, None) == 0  # n = 0: nothing to do
-    assert lib.mt_cross_entropy_rows(p, 16, p, 4, 12, p, -100, p, 1, BF16, None) == -2  # vocab not a multiple of 8
+    assert lib.mt_cross_entropy_rows(p, 16, p, 4, 0, p, -100, p, 1, BF16, None) == -2  # vocab must be positive
+    # an odd vocab needs a row stride of at least vocab rounded up to 8 (the last chunk reads the padding)
+    assert lib.mt_cross_entropy_rows(p, 13, p, 4, 13, p, -100, p, 1, BF16, None) == -3
     assert lib.mt_cross_entropy_rows(p, 8, p, 4, 16, p, -100, p, 1, BF16, None) == -3  # row stride < vocab
     assert lib.mt_cross_entropy_rows(p, 16, None, 4, 16, p, -100, p, 1, BF16, None) == -1
     assert lib.mt_cross_entropy_rows(p, 16, p, -1, 16, p, -100, p, 1, BF16, None) == -2

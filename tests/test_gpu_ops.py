@@ -352,8 +352,35 @@ def test_fused_linear_ce_edge_cases(mta):
     bad = labels.clone().cuda()
     bad[0] = 96
     assert torch.isnan(mta.ops.fused_linear_cross_entropy(h.cuda(), w.cuda(), bad))
-    with pytest.raises(ValueError, match="multiple of 8"):
-        mta.ops.fused_linear_cross_entropy(h.cuda(), w[:90].cuda(), labels.cuda())
+
+
+@pytest.mark.parametrize("vocab,compute", [(16387, "bfloat16"), (16387, "float32"), (97, "float32"), (13, "bfloat16"),
+                                           (20003, "float32")])
+def test_fused_linear_ce_odd_vocab(mta, vocab, compute):
+    """Vocabularies that are not a multiple of 8: the reference tokenizer's size is
+    3 specials plus a product with a 2-way side factor, always odd
+    (tokenizer.py:103-107).  The logits get a padded row stride; the pad columns
+    must not enter the softmax or the gradients.  20003 also takes the kernel's
+    streaming path (more than 16384 logits per row)."""
+    h, w, labels = _ce_case(300, 64, vocab, 65 + vocab % 7, ignore_every=11)
+    labels[1] = vocab - 1  # the last real column, inside the padded chunk
+    labels[2] = 0
+    hg, wg = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=compute == "bfloat16"):
+        loss = mta.ops.fused_linear_cross_entropy(hg, wg, labels.cuda())
+    loss.backward()
+    assert wg.grad.shape == (vocab, 64)
+    rl, rgh, rgw = oo.fused_linear_cross_entropy(h.numpy(), w.numpy(), labels.numpy(), -100, compute)
+    assert abs(loss.item() - rl) <= 1e-4 * abs(rl), (loss.item(), rl)
+    tol = 1e-2 if compute == "bfloat16" else 1e-4
+    assert _rel(hg.grad.cpu().numpy(), rgh) < tol
+    assert _rel(wg.grad.cpu().numpy(), rgw) < tol
+    # and the eager route the model uses for requested logits (model.py:124-129)
+    he, we = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=compute == "bfloat16"):
+        le = F.cross_entropy(F.linear(he, we), labels.cuda())
+    le.backward()
+    assert abs(loss.item() - le.item()) <= 1e-3 * abs(le.item())
 
 
 def test_fused_linear_ce_chunked_equals_single_chunk(mta, monkeypatch):
