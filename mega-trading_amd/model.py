@@ -29,6 +29,7 @@ torch ``F.linear`` + ``F.cross_entropy``.
 
 from __future__ import annotations
 
+import itertools
 import math
 
 import torch
@@ -114,8 +115,9 @@ class TradingModel(nn.Module):
 
     # KV-cached generate on the HIP routes replays one recorded HIP graph per token
     decode_graphs = True
-    # (batch, device, per-layer KV caches, recorded decode step) kept between
-    # generate calls so later calls with the same batch reuse the recording
+    # (key, per-layer KV caches, recorded decode step) kept between generate
+    # calls so later calls with the same key reuse the recording; the key is
+    # (batch, device, top_k, _recording_fingerprint())
     _gen_state = None
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
@@ -161,7 +163,9 @@ class TradingModel(nn.Module):
             return self._generate_recompute(input_ids, max_new_tokens, top_k)
         tokens = input_ids
         cache = step = None
-        key = (tokens.shape[0], tokens.device, top_k)
+        key = (tokens.shape[0], tokens.device, top_k, self._recording_fingerprint())
+        if self._gen_state is not None and self._gen_state[0] != key:
+            self._gen_state = None  # recorded against other weights, dtypes or autocast state
         for _ in range(max_new_tokens):
             t = tokens.shape[1]
             if t > self.block_size:
@@ -185,6 +189,15 @@ class TradingModel(nn.Module):
                 nxt = _sample_next(self._decode(tokens[:, -1:], cache, t - 1), top_k)
             tokens = torch.cat([tokens, nxt], dim=1)
         return tokens
+
+    def _recording_fingerprint(self):
+        """What a recorded decode step has built in besides its shapes: the
+        storage address and dtype of every parameter and buffer (the recorded
+        kernels read them by address, so ``.to(dtype)`` or
+        ``load_state_dict(assign=True)`` must not replay an old recording) and
+        the autocast state (it fixes which precision path was recorded)."""
+        tensors = tuple((t.data_ptr(), t.dtype) for t in itertools.chain(self.parameters(), self.buffers()))
+        return tensors, torch.is_autocast_enabled("cuda"), torch.get_autocast_dtype("cuda")
 
     @torch.no_grad()
     def _generate_recompute(self, input_ids: torch.Tensor, max_new_tokens: int, top_k: int) -> torch.Tensor:

@@ -199,6 +199,43 @@ def test_generate_reuses_the_recorded_step_across_calls():
     assert torch.equal(third, fresh.generate(p3, max_new_tokens=8, top_k=1))
 
 
+def test_generate_records_anew_after_weight_or_precision_changes():
+    # a recording reads the weights by address and bakes in a dtype and an
+    # autocast path: after .to(bfloat16), load_state_dict(assign=True) or a
+    # different autocast state the next call records again, and its tokens equal
+    # the graph-free path on the model as it now is
+    g = torch.Generator().manual_seed(36)
+    prompt = torch.randint(0, 128, (3, 10), generator=g).cuda()
+
+    def eager(model):
+        model.decode_graphs = False
+        try:
+            return model.generate(prompt, max_new_tokens=16, top_k=1)
+        finally:
+            model.decode_graphs = True
+
+    m = _model("hip", block_size=48)
+    m.generate(prompt, max_new_tokens=16, top_k=1)
+    state = m._gen_state
+    m.to(torch.bfloat16)
+    after_cast = m.generate(prompt, max_new_tokens=16, top_k=1)
+    assert m._gen_state is not state
+    assert torch.equal(after_cast, eager(m))
+    state = m._gen_state
+    other = _model("hip", block_size=48, seed=7).to(torch.bfloat16)
+    m.load_state_dict(other.state_dict(), assign=True)
+    after_load = m.generate(prompt, max_new_tokens=16, top_k=1)
+    assert m._gen_state is not state
+    assert torch.equal(after_load, eager(other))
+    m2 = _model("hip", block_size=48)
+    m2.generate(prompt, max_new_tokens=16, top_k=1)
+    state = m2._gen_state
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        under_amp = m2.generate(prompt, max_new_tokens=16, top_k=1)
+        assert m2._gen_state is not state
+        assert torch.equal(under_amp, eager(m2))
+
+
 def test_recorded_sampling_reproduces_the_eager_draw():
     # the recorded step samples with torch.multinomial's one-sample draw minus
     # its host-synchronising check: the same tokens for the same seed, for the
