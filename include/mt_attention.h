@@ -199,12 +199,14 @@ int mt_gqa_attn_decode_dev(const void* q, const void* k_cache, const void* v_cac
  * [B,Hq,1,D] contiguous, k_cache[:, :, pos] and v_cache[:, :, pos]
  * (cache_strides: 6 int64 = (b, h, t) of k_cache, v_cache).  With pos_dev set
  * the position is read from device memory when the kernel runs, clamped to
- * [0, pos] (pass the last valid position as pos).
+ * [0, pos] (pass the last valid position as pos).  table_rows (rows of the
+ * RoPE tables) and capacity (positions of the caches) bound pos: a pos at or
+ * past either is rejected before the launch.
  */
 int mt_decode_rope_append(const void* q, const void* k, const void* v, const int64_t* in_strides,
-                          const float* rope_cos, const float* rope_sin, int pos, const int* pos_dev, void* q_rot,
-                          void* k_cache, void* v_cache, const int64_t* cache_strides, int B, int Hq, int Hkv, int D,
-                          int in_dtype, int dtype, void* stream);
+                          const float* rope_cos, const float* rope_sin, int table_rows, int pos, const int* pos_dev,
+                          void* q_rot, void* k_cache, void* v_cache, const int64_t* cache_strides, int capacity,
+                          int B, int Hq, int Hkv, int D, int in_dtype, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -79,7 +79,8 @@ _OPS_SIGNATURES = {
     "mt_gqa_attn_decode_workspace_size": (_S, [_I, _I, _I, _I]),
     "mt_gqa_attn_decode": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _S, _P]),
     "mt_gqa_attn_decode_dev": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _F, _I, _P, _S, _P]),
-    "mt_decode_rope_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "mt_decode_rope_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                   _P]),
 }
 
 

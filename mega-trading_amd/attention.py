@@ -193,10 +193,29 @@ def decode_rope_append(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     ``cos`` / ``sin`` the fp32 RotaryEmbedding tables (row ``pos`` is used).
     ``pos`` is an int or a one-element int32 GPU tensor read when the kernel
     runs (clamped to the cache and table)."""
+    if query.device.type != "cuda":
+        raise RuntimeError("hip attention backend requires ROCm GPU tensors")
+    for t in (key, value, key_cache, value_cache, cos, sin):
+        if t.device != query.device:
+            raise RuntimeError("query, key, value, the caches and the RoPE tables must be on one device")
     if key_cache.dtype not in _KERNEL_DTYPES or value_cache.dtype != key_cache.dtype:
         raise RuntimeError("the caches must be float16 or bfloat16 and share one dtype")
     if query.dtype not in (key_cache.dtype, torch.float32) or key.dtype != query.dtype or value.dtype != query.dtype:
         raise RuntimeError("query, key and value must share one dtype: the cache dtype or float32")
+    if query.ndim != 4 or key.ndim != 4 or value.ndim != 4 or key_cache.ndim != 4 or key_cache.shape != value_cache.shape:
+        raise ValueError("query [B, Hq, 1, D], key / value [B, Hkv, 1, D], caches [B, Hkv, capacity, D]")
+    d = query.shape[-1]
+    if key.shape[-1] != d or value.shape[-1] != d or key_cache.shape[-1] != d:
+        raise ValueError("query, key, value and the caches must share head_dim")
+    for name, t in (("query", query), ("key", key), ("value", value), ("key_cache", key_cache),
+                    ("value_cache", value_cache)):
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} must have a unit last-dim stride")
+    for name, tab in (("cos", cos), ("sin", sin)):
+        if tab.shape[-1] != d // 2 or not tab.is_floating_point():
+            raise ValueError(f"RoPE {name} table must be floating point with last dimension head_dim/2 = {d // 2}")
+    # the kernel reads fp32 tables (a model cast with .to(dtype) casts its RoPE buffers too)
+    cos, sin = cos.to(torch.float32), sin.to(torch.float32)
     last = min(key_cache.shape[2], cos.reshape(-1, cos.shape[-1]).shape[0]) - 1
     if isinstance(pos, torch.Tensor):
         if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != query.device:
@@ -371,8 +390,9 @@ def decode_rope_append_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos
     cst = (ctypes.c_int64 * 6)(*k_cache.stride()[:3], *v_cache.stride()[:3])
     in_dt = _native.DTYPE_FP32 if q.dtype == torch.float32 else _KERNEL_DTYPES[q.dtype]
     with torch.cuda.device(q.device):
-        rc = lib.mt_decode_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), ins, cs.data_ptr(), sn.data_ptr(), pos,
-                                       _ptr(pos_dev), q_rot.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cst,
+        rc = lib.mt_decode_rope_append(q.data_ptr(), k.data_ptr(), v.data_ptr(), ins, cs.data_ptr(), sn.data_ptr(),
+                                       min(cs.shape[0], sn.shape[0]), pos, _ptr(pos_dev), q_rot.data_ptr(),
+                                       k_cache.data_ptr(), v_cache.data_ptr(), cst, k_cache.shape[2],
                                        b, hq, hkv, d,
                                        in_dt, _KERNEL_DTYPES[k_cache.dtype],
                                        torch.cuda.current_stream(q.device).cuda_stream)

@@ -575,9 +575,9 @@ int mt_gqa_attn_decode_dev(const void* q, const void* k_cache, const void* v_cac
 }
 
 int mt_decode_rope_append(const void* q, const void* k, const void* v, const int64_t* in_strides,
-                          const float* rope_cos, const float* rope_sin, int pos, const int* pos_dev, void* q_rot,
-                          void* k_cache, void* v_cache, const int64_t* cache_strides, int B, int Hq, int Hkv, int D,
-                          int in_dtype, int dtype, void* stream) {
+                          const float* rope_cos, const float* rope_sin, int table_rows, int pos, const int* pos_dev,
+                          void* q_rot, void* k_cache, void* v_cache, const int64_t* cache_strides, int capacity,
+                          int B, int Hq, int Hkv, int D, int in_dtype, int dtype, void* stream) {
   int rc = check_common(B, Hq, Hkv, 1, D, dtype, rope_cos, rope_sin);
   if (rc) return rc;
   if (dtype == MT_DTYPE_FP32) return fail(MT_E_DTYPE, "the KV caches must be bfloat16 or float16");
@@ -586,7 +586,12 @@ int mt_decode_rope_append(const void* q, const void* k, const void* v, const int
   if (in_dtype != MT_DTYPE_BF16 && in_dtype != MT_DTYPE_FP16 && in_dtype != 2)
     return fail(MT_E_DTYPE, "input dtype code %d unsupported", in_dtype);
   if (in_dtype != 2 && in_dtype != dtype) return fail(MT_E_DTYPE, "16-bit inputs must have the cache dtype");
-  if (pos < 0) return fail(MT_E_SHAPE, "pos must be >= 0 (got %d)", pos);
+  if (capacity < 1 || table_rows < 1)
+    return fail(MT_E_SHAPE, "cache capacity and RoPE table rows must be >= 1 (got %d, %d)", capacity, table_rows);
+  // pos is the position written (or, with pos_dev, the largest the device value is clamped to)
+  if (pos < 0 || pos >= capacity || pos >= table_rows)
+    return fail(MT_E_SHAPE, "pos %d outside the cache (capacity %d) or the RoPE table (%d rows)", pos, capacity,
+                table_rows);
   mt::RopeAppendParams p{};
   p.q = q; p.k = k; p.v = v;
   for (int i = 0; i < 2; ++i) {

@@ -29,8 +29,10 @@ torch ``F.linear`` + ``F.cross_entropy``.
 
 from __future__ import annotations
 
+import gc
 import itertools
 import math
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -515,10 +517,18 @@ class _DecodeGraph:
     replay) is harmless.  The result is the graph's static buffer, valid until
     the next call: the logits, or with ``top_k`` set the sampled next tokens
     [batch, 1] (``_sample_recorded``: the reference's top-k multinomial draw
-    without its host-side validity check, so the sampling is recorded too)."""
+    without its host-side validity check, so the sampling is recorded too).
+
+    The model is held by a weak reference: the model keeps its recording in
+    ``_gen_state``, and a strong reference back would make every generating
+    model a reference cycle that only Python's cyclic garbage collector frees,
+    at an arbitrary later moment -- possibly in the middle of another graph
+    capture, where destroying a graph or a stream is an error.  For the same
+    reason the capture runs with the cyclic collector paused, after one
+    collection of whatever dead cycles exist."""
 
     def __init__(self, model: "TradingModel", cache, batch: int, device: torch.device, top_k=None):
-        self.model = model
+        self._model = weakref.ref(model)
         self.cache = cache
         self.top_k = top_k
         self.tok = torch.zeros((batch, 1), dtype=torch.long, device=device)
@@ -527,19 +537,29 @@ class _DecodeGraph:
         self.out = None
 
     def __call__(self, token: torch.Tensor, pos: int) -> torch.Tensor:
+        model = self._model()
+        if model is None:
+            raise RuntimeError("the model of this recorded decode step no longer exists")
         self.tok.copy_(token)
         self.pos.fill_(pos)
         if self.graph is None:
             side = torch.cuda.Stream(device=self.tok.device)
             side.wait_stream(torch.cuda.current_stream(self.tok.device))
             with torch.cuda.stream(side):  # warm-up: allocator and library state outside the recording
-                self.model._decode(self.tok, self.cache, self.pos)
+                model._decode(self.tok, self.cache, self.pos)
             torch.cuda.current_stream(self.tok.device).wait_stream(side)
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
-                self.out = self.model._decode(self.tok, self.cache, self.pos)
-                if self.top_k is not None:
-                    self.out = _sample_recorded(self.out, self.top_k)
+            gc.collect()
+            was_enabled = gc.isenabled()
+            gc.disable()
+            try:
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph):
+                    self.out = model._decode(self.tok, self.cache, self.pos)
+                    if self.top_k is not None:
+                        self.out = _sample_recorded(self.out, self.top_k)
+            finally:
+                if was_enabled:
+                    gc.enable()
         self.graph.replay()
         return self.out
 

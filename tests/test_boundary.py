@@ -251,3 +251,24 @@ def test_kernel_ready_keeps_model_layout_views():
     assert ops._kernel_ready(y).is_contiguous()
     arr = ops._strides(torch.empty(1, 1, 5, 32))
     assert list(arr) == [0, 0, 32, 1]  # size-1 dims pass stride 0
+
+
+def test_decode_rope_append_bounds_pos_before_launch(mta):
+    """mt_decode_rope_append rejects a position at or past the cache capacity or
+    the RoPE table before any launch (pointers never dereferenced)."""
+    lib = mta._native.load()
+    p = 0x10000
+    ins = (ctypes.c_int64 * 6)(512, 64, 128, 64, 128, 64)
+    cst = (ctypes.c_int64 * 6)(2 * 40 * 64, 40 * 64, 64, 2 * 40 * 64, 40 * 64, 64)
+
+    def call(table_rows, pos, capacity):
+        return lib.mt_decode_rope_append(p, p, p, ins, p, p, table_rows, pos, None, p, p, p, cst, capacity,
+                                         1, 8, 2, 64, 0, 0, None)
+
+    assert call(64, 40, 40) == -2            # pos == capacity
+    assert b"capacity 40" in lib.mt_last_error()
+    assert call(20, 30, 40) == -2            # pos past the table
+    assert call(64, -1, 40) == -2
+    assert call(0, 0, 40) == -2
+    assert lib.mt_decode_rope_append(p, p, p, ins, p, p, 64, 3, None, p, p, p, cst, 40, 1, 8, 2, 64, 0, 2,
+                                     None) == -4  # fp32 caches

@@ -9,6 +9,8 @@ replay, with eager work on the same tensors in between.
 
 from __future__ import annotations
 
+import gc
+
 import importlib
 
 import pytest
@@ -94,9 +96,17 @@ def test_hip_graph_replays_match_eager():
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
 
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        static = step()
+    # dead reference cycles holding GPU objects are freed before the capture and
+    # the cyclic collector is paused during it: destroying a graph or stream
+    # while a capture is under way is an error
+    gc.collect()
+    gc.disable()
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static = step()
+    finally:
+        gc.enable()
     torch.cuda.synchronize()
 
     for replay in range(3):

@@ -145,6 +145,36 @@ def test_decode_rope_append_matches_torch_rotation(in_dt):
     assert not kc[:, :, :pos].any() and not kc[:, :, pos + 1:].any()  # only row pos written
 
 
+def test_decode_rope_append_validates_its_arguments():
+    attn = importlib.import_module("mega-trading_amd.attention")
+    b, hq, hkv, d, cap = 2, 8, 2, 64, 16
+    q = torch.zeros(b, hq, 1, d, device="cuda", dtype=torch.bfloat16)
+    k = torch.zeros(b, hkv, 1, d, device="cuda", dtype=torch.bfloat16)
+    kc = torch.zeros(b, hkv, cap, d, device="cuda", dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    rope = model_mod.RotaryEmbedding(d, 32, theta=10_000.0).cuda()
+    # a 16-bit table (a model cast with .to(dtype)) is read as fp32: same rotation as the fp32 table
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    kr = torch.randn(b, hkv, 1, d, device="cuda").to(torch.bfloat16)
+    attn.decode_rope_append(q, kr, kr, rope.cos, rope.sin, 3, kc, vc)
+    attn.decode_rope_append(q, kr, kr, rope.cos.to(torch.bfloat16).float(), rope.sin.to(torch.bfloat16).float(), 3,
+                            kc2, vc2)
+    kc3, vc3 = torch.zeros_like(kc), torch.zeros_like(vc)
+    attn.decode_rope_append(q, kr, kr, rope.cos.to(torch.bfloat16), rope.sin.to(torch.bfloat16), 3, kc3, vc3)
+    assert torch.equal(kc3, kc2) and torch.equal(vc3, vc)
+    with pytest.raises(ValueError, match="head_dim/2"):
+        attn.decode_rope_append(q, k, k, rope.cos[..., :16], rope.sin[..., :16], 3, kc, vc)
+    with pytest.raises(ValueError, match="unit last-dim stride"):
+        attn.decode_rope_append(q, k, torch.zeros(b, hkv, 1, 2 * d, device="cuda", dtype=torch.bfloat16)[..., ::2],
+                                rope.cos, rope.sin, 3, kc, vc)
+    with pytest.raises(ValueError, match="outside the cache"):
+        attn.decode_rope_append(q, k, k, rope.cos, rope.sin, cap, kc, vc)
+    with pytest.raises(RuntimeError, match="one device"):
+        attn.decode_rope_append(q, k, k, rope.cos.cpu(), rope.sin.cpu(), 3, kc, vc)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        attn.decode_rope_append(q.cpu(), k.cpu(), k.cpu(), rope.cos, rope.sin, 3, kc, vc)
+
+
 def test_graph_decode_replays_match_eager_decode():
     # one recorded decode step, replayed per position (device-side token and position), against
     # the eager step with a host position, token for token, with eager work between the replays
