@@ -29,11 +29,17 @@ import torch
 from . import _native
 
 __all__ = ["attention", "rope_attention", "rope_attention_packed", "attention_forward", "decode_attention",
-           "SUPPORTED_HEAD_DIMS", "MAX_DECODE_REPEATS"]
+           "SUPPORTED_HEAD_DIMS", "KERNEL_HEAD_DIMS", "MAX_HEAD_DIM", "MAX_DECODE_REPEATS"]
 
+# query heads per KV head one decode launch serves; larger groups run as several launches
 MAX_DECODE_REPEATS = 8
 
-SUPPORTED_HEAD_DIMS = (32, 64, 128)
+# head sizes the kernels are built for; any other head_dim up to MAX_HEAD_DIM is
+# zero-padded to the next one (the reference's forward takes any D, rounding its
+# tile to the next power of two, triton_attention.py:36)
+KERNEL_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_HEAD_DIMS = KERNEL_HEAD_DIMS
+MAX_HEAD_DIM = 128
 _KERNEL_DTYPES = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16}
 
 
@@ -101,6 +107,8 @@ def rope_attention_packed(
     _validate(q, k, v, heads // kv_heads)
     c, s = _rope_tables(cos, sin, q)
     d = q.shape[-1]
+    if d not in KERNEL_HEAD_DIMS:
+        raise ValueError(f"the packed form needs head_dim {KERNEL_HEAD_DIMS} (got {d}); use rope_attention")
     _native.load()
     out, _lse, _q_rot, _k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_packed_fwd(
         qkv, c, s, heads, kv_heads, 1.0 / math.sqrt(d))
@@ -148,7 +156,8 @@ def decode_attention(
     own included).  Returns [B, Hq, 1, D]: the last row of the causal GQA
     attention over those positions (what ``TradingModel.generate``,
     ``model.py:134-147``, obtains by recomputing the whole context).  16-bit
-    inputs; query head h reads KV head h // repeats; repeats <= 8.
+    inputs; query head h reads KV head h // repeats; head_dim 32, 64 or 128.
+    A group of more than 8 query heads per KV head runs as several launches.
 
     ``length`` is an int, or a one-element int32 tensor on the GPU that the
     kernels read when they run (clamped to [1, capacity]): the launch then
@@ -163,8 +172,8 @@ def decode_attention(
         raise ValueError("query must be [batch, heads, 1, head_dim] and the caches [batch, heads, capacity, head_dim]")
     if key_cache.shape != value_cache.shape:
         raise ValueError("key and value caches must have the same shape")
-    if key_cache.shape[1] * repeats != query.shape[1] or repeats > MAX_DECODE_REPEATS:
-        raise ValueError(f"query heads must equal key/value heads multiplied by repeats (<= {MAX_DECODE_REPEATS})")
+    if key_cache.shape[1] * repeats != query.shape[1]:
+        raise ValueError("query heads must equal key/value heads multiplied by repeats")
     if key_cache.shape[0] != query.shape[0] or key_cache.shape[3] != query.shape[3]:
         raise ValueError("query and caches must agree on batch and head_dim")
     dev_length = isinstance(length, torch.Tensor)
@@ -175,9 +184,21 @@ def decode_attention(
         raise ValueError(f"length {length} outside [1, cache capacity {key_cache.shape[2]}]")
     if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
         raise RuntimeError("query and caches must share one dtype")
-    if query.shape[-1] not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS} (got {query.shape[-1]})")
+    if query.shape[-1] not in KERNEL_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {KERNEL_HEAD_DIMS} (got {query.shape[-1]})")
     scale = 1.0 / math.sqrt(query.shape[-1])
+    if repeats > MAX_DECODE_REPEATS:
+        # the group's query heads in even sub-groups of at most MAX_DECODE_REPEATS,
+        # each one launch over the same cache (a sub-group is a GQA group of its own)
+        b, hq, _, d = query.shape
+        hkv = key_cache.shape[1]
+        n = -(-repeats // MAX_DECODE_REPEATS)
+        bounds = [repeats * j // n for j in range(n + 1)]
+        grouped = query.reshape(b, hkv, repeats, d)
+        parts = [decode_attention(grouped[:, :, lo:hi].reshape(b, hkv * (hi - lo), 1, d), key_cache, value_cache,
+                                  length, repeats=hi - lo).view(b, hkv, hi - lo, d)
+                 for lo, hi in zip(bounds[:-1], bounds[1:])]
+        return torch.cat(parts, dim=2).view(b, hq, 1, d)
     if dev_length:
         return torch.ops.mega_trading_amd.gqa_attn_decode_dev(query, key_cache, value_cache, length, scale)
     return torch.ops.mega_trading_amd.gqa_attn_decode(query, key_cache, value_cache, int(length), scale)
@@ -248,14 +269,16 @@ def _validate(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, repea
         raise RuntimeError("query, key, and value must share one dtype")
     if key.device != query.device or value.device != query.device:
         raise RuntimeError("query, key, and value must be on one device")
-    if query.shape[-1] not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS} (got {query.shape[-1]})")
+    if not 1 <= query.shape[-1] <= MAX_HEAD_DIM:
+        raise ValueError(f"head_dim must be between 1 and {MAX_HEAD_DIM} (got {query.shape[-1]})")
     if query.shape[2] < 1 or query.shape[0] < 1:
         raise ValueError("batch and sequence length must be positive")
 
 
 def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     t, d = query.shape[2], query.shape[3]
+    if d % 2:
+        raise ValueError("RoPE requires an even head dimension")
     out = []
     for name, tab in (("cos", cos), ("sin", sin)):
         if tab.shape[-1] != d // 2:
@@ -291,13 +314,46 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def _kernel_head_dim(d: int) -> int:
+    return next(x for x in KERNEL_HEAD_DIMS if x >= d)
+
+
 def _forward(q, k, v, cos, sin):
+    d = q.shape[-1]
+    dk = _kernel_head_dim(d)
+    if dk != d:
+        return _forward_padded(q, k, v, cos, sin, dk)
     _native.load()
-    scale = 1.0 / math.sqrt(q.shape[-1])
+    scale = 1.0 / math.sqrt(d)
     if cos is None:
         return torch.ops.mega_trading_amd.gqa_attn_fwd(q, k, v, scale)
     out, lse, _q_rot, _k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(q, k, v, cos, sin, scale)
     return out, lse
+
+
+def _forward_padded(q, k, v, cos, sin, dk):
+    """A head_dim the kernels are not built for, zero-padded to ``dk``: the padded
+    q / k columns add nothing to QK^T, the padded v columns produce zero output
+    columns that are dropped, the pad pairs rotate by the identity (cos 1, sin
+    0), and the scale stays 1/sqrt(head_dim).  Gradients flow back through the
+    padding.  The output keeps the query's layout."""
+    import torch.nn.functional as F
+
+    d = q.shape[-1]
+    pad = (0, dk - d)
+    qp, kp, vp = F.pad(q, pad), F.pad(k, pad), F.pad(v, pad)
+    _native.load()
+    scale = 1.0 / math.sqrt(d)
+    if cos is None:
+        out, lse = torch.ops.mega_trading_amd.gqa_attn_fwd(qp, kp, vp, scale)
+    else:
+        half = (dk - d) // 2
+        cos = F.pad(cos, (0, half), value=1.0)
+        sin = F.pad(sin, (0, half), value=0.0)
+        out, lse, _q_rot, _k_rot = torch.ops.mega_trading_amd.gqa_rope_attn_fwd(qp, kp, vp, cos, sin, scale)
+    result = torch.empty_like(q)
+    result.copy_(out[..., :d])
+    return result, lse
 
 
 # ---------------------------------------------------------------------------

@@ -39,7 +39,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import _native
-from .attention import _rope_tables
+from .attention import KERNEL_HEAD_DIMS, _rope_tables
 from .attention import attention as _hip_attention
 from .attention import decode_attention as _hip_decode_attention
 from .attention import decode_rope_append as _hip_decode_rope_append
@@ -161,7 +161,9 @@ class TradingModel(nn.Module):
         the window as the reference does.  Other backends run the reference loop.
         """
         self.eval()
-        if self.operator_backend not in HIP_BACKENDS:
+        if self.operator_backend not in HIP_BACKENDS or self.hidden_dim // self.attention_heads not in KERNEL_HEAD_DIMS:
+            # the decode kernels are built for head_dim 32 / 64 / 128; other sizes
+            # (padded in the prefill-free forward) use the reference's loop
             return self._generate_recompute(input_ids, max_new_tokens, top_k)
         tokens = input_ids
         cache = step = None
@@ -356,7 +358,7 @@ class LlamaAttention(nn.Module):
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         batch_size, sequence_length, hidden_dim = hidden.shape
         dropout_p = self.dropout if self.training else 0.0
-        if self.attention_backend == "hip" and self.fuse_rope and dropout_p == 0.0:
+        if self.attention_backend == "hip" and self.fuse_rope and dropout_p == 0.0 and self.head_dim in KERNEL_HEAD_DIMS:
             # one q|k|v GEMM whose packed output the fused-RoPE kernels read in
             # place; they write the output in the o-projection's layout and
             # the backward writes one packed q|k|v gradient

@@ -212,8 +212,14 @@ def test_validation_errors_on_device_tensors(mta):
             mta.attention(q, k, _fake((1, 2, 9, 64)), repeats=2)
         with pytest.raises(ValueError, match="agree on batch"):
             mta.attention(q, _fake((1, 2, 9, 64)), _fake((1, 2, 9, 64)), repeats=2)
-        with pytest.raises(ValueError, match="head_dim"):
-            mta.attention(_fake((1, 4, 8, 48)), _fake((1, 2, 8, 48)), _fake((1, 2, 8, 48)), repeats=2)
+        with pytest.raises(ValueError, match="head_dim must be between 1 and 128"):
+            mta.attention(_fake((1, 4, 8, 256)), _fake((1, 2, 8, 256)), _fake((1, 2, 8, 256)), repeats=2)
+        # another head size is padded to the next kernel size: the result keeps its shape
+        out48 = mta.attention(_fake((1, 4, 8, 48)), _fake((1, 2, 8, 48)), _fake((1, 2, 8, 48)), repeats=2)
+        assert out48.shape == (1, 4, 8, 48)
+        with pytest.raises(ValueError, match="even head dimension"):
+            mta.rope_attention(_fake((1, 4, 8, 9)), _fake((1, 2, 8, 9)), _fake((1, 2, 8, 9)),
+                               torch.empty(8, 4, device="cuda"), torch.empty(8, 4, device="cuda"), repeats=2)
         with pytest.raises(RuntimeError, match="share one dtype"):
             mta.attention(q, _fake((1, 2, 8, 64), torch.float16), k, repeats=2)
         cos = torch.empty(4, 32, device="cuda")

@@ -63,11 +63,29 @@ def test_decode_attention_strided_views_and_errors():
     with pytest.raises(ValueError, match="length"):
         mta.decode_attention(q, kc, vc, 65, repeats=4)
     with pytest.raises(ValueError, match="repeats"):
-        mta.decode_attention(torch.zeros(1, 32, 1, 64, device="cuda", dtype=torch.bfloat16),
+        mta.decode_attention(torch.zeros(1, 24, 1, 64, device="cuda", dtype=torch.bfloat16),
                              torch.zeros(1, 2, 8, 64, device="cuda", dtype=torch.bfloat16),
                              torch.zeros(1, 2, 8, 64, device="cuda", dtype=torch.bfloat16), 4, repeats=16)
     with pytest.raises(RuntimeError, match="float16 and bfloat16"):
         mta.decode_attention(q.float(), kc, vc, 4, repeats=4)
+
+
+@pytest.mark.parametrize("hq,hkv,length", [(32, 2, 300), (12, 1, 77), (28, 4, 513)])
+def test_decode_attention_groups_larger_than_one_launch(hq, hkv, length):
+    # more than 8 query heads per KV head (the reference's modal config has 7; any
+    # R works there): the group runs as several launches of at most 8 heads
+    g = torch.Generator().manual_seed(hq + length)
+    b, d, cap = 2, 64, 600
+    q = (torch.randn(b, hq, 1, d, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    kc = (torch.randn(b, hkv, cap, d, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    vc = (torch.randn(b, hkv, cap, d, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    r = hq // hkv
+    ref = orc.decode_attention(q[:, :, 0].double().cpu().numpy(), kc.double().cpu().numpy(),
+                               vc.double().cpu().numpy(), length, r)
+    for ln in (length, torch.tensor([length], dtype=torch.int32, device="cuda")):
+        out = mta.decode_attention(q, kc, vc, ln, repeats=r)
+        assert out.shape == (b, hq, 1, d)
+        assert np.abs(out[:, :, 0].double().cpu().numpy() - ref).max() <= 2e-2
 
 
 def _model(backend, block_size=64, seed=0, **kw):

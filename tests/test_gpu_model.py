@@ -159,3 +159,27 @@ def test_fp32_model_without_autocast_matches_the_sdpa_route():
     worst = max(_rel(g_hip[n], g_ref[n]) for n in g_ref)
     print(f"worst fp32 grad rel err {worst:.3e}")
     assert worst <= 1e-4
+
+
+def test_demo_ablation_model_with_head_dim_8():
+    """The reference's demo ablation sizes (configs/ablations/demo.yaml:24-31:
+    hidden 16 with 2 heads, head_dim 8) on the "triton" route: the attention runs
+    zero-padded to the 32-wide kernels, loss and gradients match the SDPA route,
+    and generate (the reference's recompute loop at this head size) runs."""
+    cfg = dict(vocab_size=64, block_size=128, hidden_dim=16, layers=1, attention_heads=2, kv_heads=2,
+               intermediate_dim=48, dropout=0.0, rope_theta=10_000.0)
+    ids, labels = workload.zipf_batch(4, 96, cfg["vocab_size"], seed=8)
+    ids, labels = ids.cuda(), labels.cuda()
+    out = {}
+    for route in ("auto", "triton"):
+        m = workload.build_model(route, seed=0, device="cuda", **cfg)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            loss, _ = m.forward_with_loss(ids, labels, return_logits=True)
+        loss.backward()
+        out[route] = (loss.detach().float(), {n: p.grad.detach().float().clone() for n, p in m.named_parameters()})
+    (l_ref, g_ref), (l_hip, g_hip) = out["auto"], out["triton"]
+    assert abs(l_hip.item() - l_ref.item()) <= TOL_LOSS_REL * abs(l_ref.item())
+    assert max(_rel(g_hip[n], g_ref[n]) for n in g_ref) <= TOL_GRAD_REL
+    m = workload.build_model("triton", seed=0, device="cuda", **cfg)
+    gen = m.generate(ids[:2, :20], max_new_tokens=8, top_k=4)
+    assert gen.shape == (2, 28)

@@ -275,3 +275,28 @@ def test_native_library_is_loaded(mta):
     maps = open("/proc/self/maps").read()
     assert mta._native.library_path() in maps
     assert mta._native.torch_ops_path() in maps
+
+
+@pytest.mark.parametrize("d", [8, 16, 40, 48, 80, 100, 17])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_other_head_dims_are_padded_to_a_kernel_size(mta, d, dtype):
+    """Head sizes the kernels are not built for (the reference's forward takes any
+    D, triton_attention.py:36; its demo ablation uses D = 8, configs/ablations/
+    demo.yaml:24-31) run zero-padded to the next of 32 / 64 / 128 with the scale of
+    the real D.  RoPE needs an even D (17 runs without it)."""
+    t, hq, hkv = 150, 6, 2
+    q, k, v, do = make_inputs(2, t, hq, hkv, d, sigma=0.5, seed=d, dtype=dtype)
+    tol = dict(out_tol=1e-4, grad_tol=1e-4, lse_tol=1e-4) if dtype == torch.float32 else {}
+    compare(run_hip(mta, q, k, v, do, 3), oracle(q, k, v, do, 3), **tol)
+    if d % 2 == 0:
+        cos, sin = orc.rope_tables(t, d, 10_000.0)
+        compare(run_hip(mta, q, k, v, do, 3, cos, sin), oracle(q, k, v, do, 3, cos, sin), **tol)
+
+
+def test_padded_head_dim_keeps_the_query_layout(mta):
+    b, t, hq, hkv, d = 2, 64, 4, 2, 8
+    q, k, v, do = make_inputs(b, t, hq, hkv, d, seed=3)
+    dev = "cuda:0"
+    qv = q.transpose(1, 2).contiguous().to(dev).transpose(1, 2).requires_grad_(True)
+    out = mta.attention(qv, k.to(dev), v.to(dev), repeats=2)
+    assert out.shape == qv.shape and out.stride() == qv.stride()
