@@ -72,19 +72,25 @@ def test_fused_rope_route_passes_fp32_tables_and_raw_qk():
 
 
 def test_hip_route_passes_the_packed_qkv_product_in_16_bits():
-    # 16-bit activations (the autocast case): one q|k|v GEMM whose packed
-    # output goes to the packed fused-RoPE op; fp32 keeps the head views
-    attention = _attn("hip").to(torch.bfloat16)
-    hidden = torch.randn(1, 8, 16).to(torch.bfloat16)
+    # 16-bit activations (the autocast case) and a kernel head size: one q|k|v
+    # GEMM whose packed output goes to the packed fused-RoPE op; fp32 keeps the
+    # head views, and so does a head size the kernels pad (head_dim 4 here)
+    attention = _attn("hip", hidden_dim=128).to(torch.bfloat16)  # 4 heads of 32
+    hidden = torch.randn(1, 8, 128).to(torch.bfloat16)
     with patch("mega-trading_amd.model._hip_rope_attention_packed",
-               return_value=torch.zeros(1, 8, 16, dtype=torch.bfloat16)) as op:
+               return_value=torch.zeros(1, 8, 128, dtype=torch.bfloat16)) as op:
         out = attention(hidden)
     qkv, cos, sin = op.call_args.args[:3]
-    assert out.shape == hidden.shape and qkv.shape == (1, 8, 16 + 8 + 8)
+    assert out.shape == hidden.shape and qkv.shape == (1, 8, 128 + 64 + 64)
     assert op.call_args.kwargs == {"heads": 4, "kv_heads": 2}
     assert cos is attention.rope.cos and sin is attention.rope.sin
     want = torch.cat([attention.q_proj(hidden), attention.k_proj(hidden), attention.v_proj(hidden)], dim=-1)
     torch.testing.assert_close(qkv, want)
+    small = _attn("hip").to(torch.bfloat16)  # head_dim 4
+    with patch("mega-trading_amd.model._hip_rope_attention",
+               return_value=torch.zeros(1, 4, 8, 4, dtype=torch.bfloat16)) as op2:
+        small(torch.randn(1, 8, 16).to(torch.bfloat16))
+    assert op2.call_args.args[0].shape == (1, 4, 8, 4)
 
 
 def test_dropout_in_training_falls_back_to_sdpa():
