@@ -115,19 +115,26 @@ def test_cached_logits_match_full_recompute(backend):
 
 
 def test_generate_greedy_matches_recompute_and_crosses_the_window():
+    # the cached HIP generation against the reference's loop (model.py:134-147) on
+    # the same weights, recomputed through the HIP route and through the SDPA
+    # route: greedy tokens equal wherever the recompute's top-2 gap is clear of
+    # the bf16 attention's rounding
     m = _model("hip", block_size=32)
     for p in m.output.parameters():  # sharper logits: fewer near-ties between top-2 tokens
         p.data.mul_(25.0)
+    sdpa = _model("auto", block_size=32)
+    sdpa.load_state_dict(m.state_dict())
     g = torch.Generator().manual_seed(12)
     prompt = torch.randint(0, 128, (4, 12), generator=g).cuda()
     out = m.generate(prompt, max_new_tokens=30, top_k=1)  # 12 + 30 > 32: the window slides
     assert out.shape == (4, 42) and torch.equal(out[:, :12], prompt)
     with torch.no_grad():
-        for t in range(12, 42):
-            full = m(out[:, max(0, t - 32):t])[:, -1, :]
-            top2 = full.topk(2, dim=-1).values
-            clear = (top2[:, 0] - top2[:, 1]) > 5e-2 * top2[:, 0].abs().clamp_min(1.0)
-            assert torch.equal(out[clear, t], full.argmax(-1)[clear]), t
+        for ref_model in (m, sdpa):
+            for t in range(12, 42):
+                full = ref_model(out[:, max(0, t - 32):t])[:, -1, :]
+                top2 = full.topk(2, dim=-1).values
+                clear = (top2[:, 0] - top2[:, 1]) > 5e-2 * top2[:, 0].abs().clamp_min(1.0)
+                assert torch.equal(out[clear, t], full.argmax(-1)[clear]), (ref_model.operator_backend, t)
 
 
 def test_generate_sampling_runs_at_c5_shape():

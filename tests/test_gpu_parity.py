@@ -31,8 +31,13 @@ from tests.gpu_cases import (
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
-# (batch, kv group) slices checked against the oracle at full size
-SAMPLES = {"C1": [(0, 0), (1, 1)], "C2": [(0, 0), (15, 1)], "C3": [(3, 1)], "C4": [(7, 5)]}
+# (batch, kv group) slices checked against the oracle at full size.  The grids
+# issue (batch 0, group 0) first and (last batch, last group) last -- in every
+# kernel the workgroup index runs over (batch, group) fastest, longest causal
+# work first -- so those two slices hold the first and the last workgroups in
+# issue order; the others are interior.
+SAMPLES = {"C1": [(0, 0), (1, 1)], "C2": [(0, 0), (15, 1), (7, 0)],
+           "C3": [(0, 0), (3, 3), (1, 2), (3, 1)], "C4": [(0, 0), (7, 7), (3, 4), (7, 5)]}
 
 
 @pytest.mark.parametrize("rope", [False, True], ids=["plain", "rope"])
