@@ -62,13 +62,18 @@ C3 = (4, 4096, 16, 4, 64)
 C4 = (8, 2048, 32, 8, 128)
 
 # algorithmic MFMA FLOPs per launch, in units of B * Hq * D * T(T+1)/2
+# FLOPs per launch in units of B*Hq*D*T(T+1)/2.  "algorithmic" is the work the
+# metric credits (forward 4, backward 10: the FlashAttention convention, 14 per
+# fwd+bwd step); "executed" what the kernel actually issues: the backward
+# computes S and dP twice, once for its dQ tasks and once for its dK/dV tasks.
 KERNEL_FLOP_UNITS = {
-    "attn_fwd_kernel": 4,      # S = QK^T, O = PV
+    "attn_fwd_kernel": (4, 4),      # S = QK^T, O = PV
     # the backward (D <= 64): dQ tasks and dK/dV tasks in one launch
-    "attn_bwd_kernel": 14,
-    # the same kernel launched with one kind of task only (diagnostic split)
-    "attn_bwd_kernel[dq]": 6,   # S, dP recomputed; dQ = dS K
-    "attn_bwd_kernel[dkv]": 8,  # S, dP recomputed; dV = P^T dO, dK = dS^T Q
+    "attn_bwd_kernel": (10, 14),
+    # the same kernel launched with one kind of task only (a diagnostic: the
+    # half-backward entry points); credited with what they execute
+    "attn_bwd_kernel[dq]": (6, 6),   # S, dP recomputed; dQ = dS K
+    "attn_bwd_kernel[dkv]": (8, 8),  # S, dP recomputed; dV = P^T dO, dK = dS^T Q
 }
 
 
@@ -312,9 +317,9 @@ def time_kernels(pkg, cfg, iters):
         e1.record(stream)
         torch.cuda.synchronize()
         stage_ms = e0.elapsed_time(e1) / iters
-        flops = KERNEL_FLOP_UNITS[name] * b * hq * d * pairs(t)
-        out[name] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "algorithmic_flop": flops,
-                     "stage_ms": stage_ms}
+        alg, exe = (u * b * hq * d * pairs(t) for u in KERNEL_FLOP_UNITS[name])
+        out[name] = {"ms": ms, "tflops": alg / (ms * 1e-3) / 1e12, "algorithmic_flop": alg,
+                     "executed_tflops": exe / (ms * 1e-3) / 1e12, "stage_ms": stage_ms}
     return out
 
 
@@ -666,7 +671,8 @@ def main(argv=None) -> int:
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": hbm_traffic(dom),
         },
-        "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1), "stage_ms": round(x["stage_ms"], 4)}
+        "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1),
+                        "executed_tflops": round(x["executed_tflops"], 1), "stage_ms": round(x["stage_ms"], 4)}
                     for n, x in kern.items()},
         "mfma_ceiling": ceiling,
         "ops": ops_line,

@@ -1,8 +1,9 @@
 /*
  * C ABI of the decoder operators around the attention (also in
- * libmt_attn.so): RMSNorm, residual-add + RMSNorm and the SwiGLU gate,
- * forward and backward, and the cross-entropy rows of the fused linear
- * cross-entropy loss head, for MI355X (gfx950).  Plain pointers and sizes only.
+ * libmt_attn.so): RMSNorm, residual-add + RMSNorm, the SwiGLU gate and the
+ * stand-alone RoPE, forward and backward, and the cross-entropy rows of the
+ * fused linear cross-entropy loss head, for MI355X (gfx950).  Plain pointers
+ * and sizes only.
  *
  * They replace these reference operators (src/mega_trading/kernels/triton_ops.py):
  *
@@ -24,6 +25,10 @@
  *   mt_swiglu_packed_fwd / _bwd  no counterpart: the same gate on the packed
  *                           output of one GEMM against the stacked (w1; w3)
  *                           weights (this build's "hip" decoder route)
+ *   mt_apply_rope        <- _TritonRoPE.forward / .backward :187-214 (kernel
+ *                           _rope_kernel :690-761, launcher :477-525), reached
+ *                           from triton_apply_rope :45-54 and
+ *                           RotaryEmbedding.forward, src/mega_trading/model.py:292-293
  *   mt_cross_entropy_rows <- _fused_ce_row_kernel :822-887, the per-chunk loss and
  *                           in-place logits-gradient step of
  *                           _TritonFusedLinearCrossEntropy.forward :312-400,
@@ -142,6 +147,19 @@ int mt_swiglu_packed_bwd(const void* gu, const void* dout, void* dgu, int64_t ro
 int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* labels, int64_t rows, int vocab,
                           const int64_t* n_valid, int64_t ignore_index, float* loss_rows, int write_grad, int dtype,
                           void* stream);
+
+/* Stand-alone RoPE of q [B, Hq, T, D] and k [B, Hkv, T, D]: each
+ * interleaved pair (x[2i], x[2i+1]) = (e, o) of row t becomes
+ *   (e c - o s, e s + o c),  c = rope_cos[t * table_stride + i], s = rope_sin[...]
+ * with s negated when inverse != 0 (the backward: gradients rotated by -theta,
+ * the reference's NEGATE_SIN).  strides: 16 element strides, (b, h, t, d) of
+ * q, q_out, k, k_out in that order; any values (rows with d stride 1, D % 8 == 0
+ * and 16-byte alignment take 8-value vector accesses).  An output may be its
+ * input (same pointer and strides).  Tables fp32, d stride 1, at least T rows.
+ * D even; arithmetic fp32, one rounding to dtype per value. */
+int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B, int Hq, int Hkv, int T, int D,
+                  const int64_t* strides, const float* rope_cos, const float* rope_sin, int64_t table_stride,
+                  int table_rows, int inverse, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -45,6 +45,7 @@ EXPORTS = (
     "mt_swiglu_packed_fwd",
     "mt_swiglu_packed_bwd",
     "mt_cross_entropy_rows",
+    "mt_apply_rope",
     "mt_gqa_attn_decode_workspace_size",
     "mt_gqa_attn_decode",
     "mt_gqa_attn_decode_dev",
@@ -76,6 +77,7 @@ _OPS_SIGNATURES = {
     "mt_swiglu_packed_fwd": (_I, [_P, _P, _L, _L, _I, _P]),
     "mt_swiglu_packed_bwd": (_I, [_P, _P, _P, _L, _L, _I, _P]),
     "mt_cross_entropy_rows": (_I, [_P, _L, _P, _L, _I, _P, _L, _P, _I, _I, _P]),
+    "mt_apply_rope": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _L, _I, _I, _I, _P]),
     "mt_gqa_attn_decode_workspace_size": (_S, [_I, _I, _I, _I]),
     "mt_gqa_attn_decode": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _S, _P]),
     "mt_gqa_attn_decode_dev": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _F, _I, _P, _S, _P]),

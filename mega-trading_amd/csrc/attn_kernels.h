@@ -1441,11 +1441,19 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
 // Backward, dQ and dK/dV work in one launch (D <= 64)
 // ===========================================================================
 // The n_kv dK/dV tasks and the n_dq dQ tasks are independent once the prep
-// pass has written -delta and -LSE log2(e), so one grid holds both: block L
-// is a dK/dV task when the proportional interleave floor(L n_kv / N) steps
-// at L, else a dQ task.  Both task lists are heaviest first, so the merged
-// order is close to heaviest first overall and the light tasks of either kind
-// fill the slots the other kind's long tasks leave at the end.
+// pass has written -delta and -LSE log2(e), so one grid holds both, merged by
+// a proportional interleave (a dK/dV task where floor(i n_kv / N) steps).
+// Both task lists are heaviest first, so the merged order is close to
+// heaviest first overall and the light tasks of either kind fill the slots
+// the other kind's long tasks leave at the end.
+//
+// Workgroups are dealt to the 8 XCDs round-robin by index, and both task
+// lists give task i the (batch, KV head) group i mod (B Hkv) (times the
+// head split), so with 8 | B Hkv a task's group decides its XCD.  The merge
+// keeps that: it interleaves chunks of 8 consecutive workgroups, each chunk
+// one kind, so task index and workgroup index agree mod 8 and the dQ and
+// dK/dV tasks of a group share one XCD's L2 (its K/V and Q/dO rows).  When a
+// count is not a multiple of 8 the merge is per workgroup.
 template <int D>
 struct BwdLds {
   static constexpr int BYTES = DqLds<D>::BYTES > DkvLds<D>::BYTES ? DqLds<D>::BYTES : DkvLds<D>::BYTES;
@@ -1456,13 +1464,17 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnParams p) {
   static_assert(kKvWaves == 4, "dQ and dK/dV workgroups must have the same size");
   __shared__ __attribute__((aligned(1024))) char lds[BwdLds<D>::BYTES];
   const int L = blockIdx.x;
-  const int n = p.n_kv_tasks + p.n_dq_tasks;
-  const int kv_before = (int)((int64_t)L * p.n_kv_tasks / n);
-  const int kv_through = (int)((int64_t)(L + 1) * p.n_kv_tasks / n);
+  const int sh = ((p.n_kv_tasks | p.n_dq_tasks) & 7) == 0 ? 3 : 0;  // chunks of 8 workgroups, or of 1
+  const int c = L >> sh;
+  const int n = (p.n_kv_tasks + p.n_dq_tasks) >> sh;
+  const int nkv = p.n_kv_tasks >> sh;
+  const int kv_before = (int)((int64_t)c * nkv / n);
+  const int kv_through = (int)((int64_t)(c + 1) * nkv / n);
+  const int sub = L - (c << sh);
   if (kv_through > kv_before)
-    dkv_body<E, D, ROPE>(p, kv_before, lds);
+    dkv_body<E, D, ROPE>(p, (kv_before << sh) + sub, lds);
   else
-    dq_body<E, D, ROPE, PEEL>(p, L - kv_before, lds);
+    dq_body<E, D, ROPE, PEEL>(p, ((c - kv_before) << sh) + sub, lds);
 }
 
 // ===========================================================================

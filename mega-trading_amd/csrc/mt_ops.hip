@@ -1,5 +1,5 @@
 // C ABI of the decoder operators (RMSNorm, residual-add + RMSNorm, SwiGLU
-// gate, cross-entropy rows): argument checks, launch geometry and dispatch to
+// gate, cross-entropy rows, stand-alone RoPE): argument checks, launch geometry and dispatch to
 // ops_kernels.h.
 // Declared in include/mt_ops.h.
 #include <hip/hip_runtime.h>
@@ -226,6 +226,14 @@ int rms_bwd_common(const void* s, const void* w, const float* rstd, const void* 
   return MT_OK;
 }
 
+}  // namespace
+
+namespace {
+template <int DT>
+void rope_launch(bool vec, dim3 grid, hipStream_t st, const K::RopeArgs& a) {
+  if (vec) hipLaunchKernelGGL((K::rope_kernel<DT, true>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((K::rope_kernel<DT, false>), grid, dim3(256), 0, st, a);
+}
 }  // namespace
 
 extern "C" {
@@ -458,6 +466,59 @@ int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* label
   if (dtype == MT_DTYPE_BF16) ce_dispatch<K::kDtBF16>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
   else if (dtype == MT_DTYPE_FP16) ce_dispatch<K::kDtFP16>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
   else ce_dispatch<K::kDtFP32>(nch, write_grad != 0, grid, st, logits, row_stride, labels, vocab, n_valid, ignore_index, loss_rows);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B, int Hq, int Hkv, int T, int D,
+                  const int64_t* strides, const float* rope_cos, const float* rope_sin, int64_t table_stride,
+                  int table_rows, int inverse, int dtype, void* stream) {
+  int rc;
+  if ((rc = check_dtype(dtype, dtype))) return rc;
+  if (B < 0 || Hq < 0 || Hkv < 0 || T < 0)
+    return fail(MT_E_SHAPE, "B, Hq, Hkv and T must be >= 0 (got %d, %d, %d, %d)", B, Hq, Hkv, T);
+  if (D < 2 || D % 2) return fail(MT_E_SHAPE, "RoPE requires an even head dimension (got %d)", D);
+  if (table_rows < T) return fail(MT_E_ROPE, "RoPE tables have %d rows, fewer than T = %d", table_rows, T);
+  if (table_stride < D / 2) return fail(MT_E_ROPE, "RoPE table row stride %lld below D / 2 = %d",
+                                        (long long)table_stride, D / 2);
+  const int64_t rows_q = (int64_t)B * Hq * T, rows_k = (int64_t)B * Hkv * T;
+  if (rows_q + rows_k == 0) return ok();
+  if (!strides || !rope_cos || !rope_sin) return fail(MT_E_NULL, "strides, rope_cos and rope_sin must be non-NULL");
+  if ((rows_q && (!q || !q_out)) || (rows_k && (!k || !k_out))) return fail(MT_E_NULL, "q, k, q_out and k_out must be non-NULL");
+  K::RopeArgs a;
+  a.src[0] = q;
+  a.src[1] = k;
+  a.dst[0] = q_out;
+  a.dst[1] = k_out;
+  bool vec = D % 8 == 0 && aligned16(rope_cos) && aligned16(rope_sin) && table_stride % 4 == 0;
+  for (int w = 0; w < 2; ++w)
+    for (int j = 0; j < 4; ++j) {
+      a.ss[w][j] = strides[8 * w + j];
+      a.sd[w][j] = strides[8 * w + 4 + j];
+    }
+  for (int w = 0; w < 2; ++w) {
+    if (w == 0 ? rows_q == 0 : rows_k == 0) continue;
+    vec = vec && a.ss[w][3] == 1 && a.sd[w][3] == 1 && aligned16(a.src[w]) && aligned16(a.dst[w]);
+    for (int j = 0; j < 3; ++j) vec = vec && a.ss[w][j] % 8 == 0 && a.sd[w][j] % 8 == 0;
+  }
+  a.heads[0] = Hq > 0 ? Hq : 1;
+  a.heads[1] = Hkv > 0 ? Hkv : 1;
+  a.T = T;
+  a.half = D / 2;
+  a.cos = rope_cos;
+  a.sin = rope_sin;
+  a.tstride = table_stride;
+  a.sign = inverse ? -1.f : 1.f;
+  const int per_row = vec ? D / 8 : D / 2;
+  a.n0 = rows_q * per_row;
+  a.n = a.n0 + rows_k * per_row;
+  const int64_t blocks = (a.n + 255) / 256;
+  if (blocks > 0x7fffffffLL) return fail(MT_E_SHAPE, "too many pairs (%lld)", (long long)(a.n));
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks);
+  if (dtype == MT_DTYPE_BF16) rope_launch<K::kDtBF16>(vec, grid, st, a);
+  else if (dtype == MT_DTYPE_FP16) rope_launch<K::kDtFP16>(vec, grid, st, a);
+  else rope_launch<K::kDtFP32>(vec, grid, st, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }

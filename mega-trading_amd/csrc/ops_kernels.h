@@ -1,12 +1,13 @@
 // gfx950 kernels for the decoder's memory-bound operators around the
-// attention: RMSNorm (optionally fused with the residual add) and the SwiGLU
-// gate, forward and backward.
+// attention: RMSNorm (optionally fused with the residual add), the SwiGLU
+// gate and the stand-alone RoPE, forward and backward.
 //
 // Reference operators (src/mega_trading/kernels/triton_ops.py):
 //   RMSNorm          :11-15, :133-184, kernels :528-539 (forward), :633-666 (backward)
 //   add + RMSNorm    :18-42, :217-291, kernels :541-566, :569-608
 //   SwiGLU gate      :57-61, :431-474, kernels :774-782, :799-819
 //   cross-entropy rows of the fused linear cross-entropy :294-412, kernel :822-887
+//   RoPE             :45-54, :187-214, kernel :690-761
 //
 // All of them move each byte once: one wave owns one row (RMSNorm, rows of D
 // <= 4096 values held in registers as 8-value chunks), the SwiGLU gate streams
@@ -546,6 +547,71 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(void* logits, int64_t ld, 
         grad8(c, v[0]);
       }
     }
+  }
+}
+
+// ===========================================================================
+// Stand-alone RoPE (triton_ops.py:187-214, kernel :690-761): every
+// interleaved pair (e, o) of q and k becomes (e c - o s, e s + o c), with s
+// negated for the backward (a rotation by -theta).  One launch covers the
+// B*Hq*T query rows, then the B*Hkv*T key rows.  VEC (every d stride 1,
+// D % 8 == 0, 16-byte aligned rows and table rows): a lane takes 8 values (4
+// pairs); otherwise a lane takes one pair, any strides.  A lane reads its
+// values before writing the same positions, so the output may be the input.
+// ===========================================================================
+struct RopeArgs {
+  const void* src[2];  // q, k
+  void* dst[2];        // q_out, k_out
+  int64_t ss[2][4];    // (b, h, t, d) element strides of src
+  int64_t sd[2][4];    // ... of dst
+  int heads[2];        // Hq, Hkv
+  int T;
+  int half;            // D / 2
+  const float* cos;    // [rows >= T, D / 2], row stride tstride, d stride 1
+  const float* sin;
+  int64_t tstride;
+  float sign;          // +1 forward, -1 inverse
+  int64_t n0;          // lane units of q
+  int64_t n;           // lane units of q and k
+};
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= a.n) return;
+  const int w = u >= a.n0 ? 1 : 0;
+  const int64_t local = u - (w ? a.n0 : 0);
+  constexpr int P = VEC ? 4 : 1;  // pairs per lane
+  const int per_row = a.half / P;
+  const int i = int(local % per_row) * P;  // first pair
+  const int64_t row = local / per_row;
+  const int t = int(row % a.T);
+  const int64_t bh = row / a.T;
+  const int h = int(bh % a.heads[w]);
+  const int64_t b = bh / a.heads[w];
+  const int64_t so = b * a.ss[w][0] + h * a.ss[w][1] + t * a.ss[w][2];
+  const int64_t dO = b * a.sd[w][0] + h * a.sd[w][1] + t * a.sd[w][2];
+  const float* cp = a.cos + t * a.tstride + i;
+  const float* sp = a.sin + t * a.tstride + i;
+  if constexpr (VEC) {
+    float v[8];
+    IO<DT>::load8(a.src[w], so + 2 * i, v);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(cp);
+    const f32x4 s = *reinterpret_cast<const f32x4*>(sp);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float e = v[2 * p], o = v[2 * p + 1], sn = s[p] * a.sign;
+      v[2 * p] = e * c[p] - o * sn;
+      v[2 * p + 1] = e * sn + o * c[p];
+    }
+    IO<DT>::store8(a.dst[w], dO + 2 * i, v);
+  } else {
+    const int64_t sdd = a.ss[w][3], ddd = a.sd[w][3];
+    const float e = IO<DT>::load1(a.src[w], so + 2 * i * sdd);
+    const float o = IO<DT>::load1(a.src[w], so + (2 * i + 1) * sdd);
+    const float c = *cp, sn = *sp * a.sign;
+    IO<DT>::store1(a.dst[w], dO + 2 * i * ddd, e * c - o * sn);
+    IO<DT>::store1(a.dst[w], dO + (2 * i + 1) * ddd, e * sn + o * c);
   }
 }
 

@@ -13,8 +13,10 @@ The module tree, argument names and routing follow the reference model
 * ``"triton"`` (the reference's value, kept so its configs work unchanged) or
   ``"hip"`` with ``dropout_p == 0`` (``model.py:225``): the gfx950 kernels.  By
   default RoPE is fused into them (``rope_attention`` with the fp32 tables);
-  ``fuse_rope=False`` keeps the reference's two calls, ``self.rope`` then
-  ``attention(query, key, value, repeats=...)`` (``model.py:223,226``).
+  ``fuse_rope=False`` keeps the reference's two calls, ``self.rope`` (on
+  the HIP RoPE kernel, ``ops.apply_rope``, as the reference's RotaryEmbedding
+  takes the attention backend) then ``attention(query, key, value,
+  repeats=...)`` (``model.py:213,223,226``).
 
 The other operators follow the reference's routing too: the SwiGLU gate
 takes the attention backend (``model.py:179-183, 252-253``), so "triton" /
@@ -47,6 +49,7 @@ from .attention import rope_attention as _hip_rope_attention
 from .attention import rope_attention_packed as _hip_rope_attention_packed
 from .ops import fused_linear_cross_entropy as _hip_fused_linear_cross_entropy
 from .ops import add_rms_norm as _hip_add_rms_norm
+from .ops import apply_rope as _hip_apply_rope
 from .ops import add_rms_norm_mixed as _hip_add_rms_norm_mixed
 from .ops import rms_norm as _hip_rms_norm
 from .ops import rms_norm_mixed as _hip_rms_norm_mixed
@@ -349,7 +352,7 @@ class LlamaAttention(nn.Module):
         self.k_proj = nn.Linear(hidden_dim, kv_heads * self.head_dim, bias=False)
         self.v_proj = nn.Linear(hidden_dim, kv_heads * self.head_dim, bias=False)
         self.o_proj = nn.Linear(hidden_dim, hidden_dim, bias=False)
-        self.rope = RotaryEmbedding(self.head_dim, block_size, theta=rope_theta)
+        self.rope = RotaryEmbedding(self.head_dim, block_size, theta=rope_theta, operator_backend=attention_backend)
         self.dropout = dropout
         self.rope_theta = rope_theta
         self.attention_backend = attention_backend
@@ -487,12 +490,18 @@ def _norm_backend(attention_backend: str) -> str:
 
 
 class RotaryEmbedding(nn.Module):
-    """fp32 tables cos/sin [1, 1, T_max, D/2] of pos * theta^(-2i/D) (``model.py:272-294``)."""
+    """fp32 tables cos/sin [1, 1, T_max, D/2] of pos * theta^(-2i/D) (``model.py:272-294``).
 
-    def __init__(self, head_dim: int, max_sequence_length: int, theta: float) -> None:
+    ``operator_backend`` "triton" or "hip" rotates with the HIP RoPE kernel
+    (``ops.apply_rope``, in place of ``triton_apply_rope``, ``model.py:292-293``);
+    any other value with torch.  Both take the tables cast to the activation
+    dtype, as the reference does."""
+
+    def __init__(self, head_dim: int, max_sequence_length: int, theta: float, operator_backend: str = "auto") -> None:
         super().__init__()
         if head_dim % 2 != 0:
             raise ValueError("RoPE requires an even head dimension")
+        self.operator_backend = operator_backend
         positions = torch.arange(max_sequence_length, dtype=torch.float32)
         inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
         freqs = torch.outer(positions, inv_freq)
@@ -505,6 +514,8 @@ class RotaryEmbedding(nn.Module):
             raise ValueError(f"sequence length {sequence_length} exceeds RoPE cache length {self.cos.shape[-2]}")
         cos = self.cos[:, :, :sequence_length].to(dtype=query.dtype)
         sin = self.sin[:, :, :sequence_length].to(dtype=query.dtype)
+        if self.operator_backend in HIP_BACKENDS:
+            return _hip_apply_rope(query, key, cos, sin)
         return rotate(query, cos, sin), rotate(key, cos, sin)
 
 

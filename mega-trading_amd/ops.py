@@ -6,6 +6,7 @@ Drop-ins for the reference's operator functions in
 * ``rms_norm(hidden, weight, *, eps)``            <- ``triton_rms_norm`` (:11-15)
 * ``add_rms_norm(hidden, residual, weight, *, eps)`` <- ``triton_add_rms_norm`` (:18-42)
 * ``swiglu_gate(gate, up)``                       <- ``triton_swiglu_gate`` (:57-61)
+* ``apply_rope(query, key, cos, sin)``            <- ``triton_apply_rope`` (:45-54)
 * ``fused_linear_cross_entropy(hidden, weight, labels, *, ignore_index)``
                                                   <- ``triton_fused_linear_cross_entropy`` (:64-92)
 
@@ -21,6 +22,7 @@ registered backward, launched on the caller's current stream.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -29,7 +31,7 @@ from . import _native
 from .gemm_tuning import tuned_gemms
 
 __all__ = ["rms_norm", "add_rms_norm", "rms_norm_mixed", "add_rms_norm_mixed", "swiglu_gate", "swiglu_gate_packed",
-           "fused_linear_cross_entropy", "MAX_NORM_DIM"]
+           "apply_rope", "fused_linear_cross_entropy", "MAX_NORM_DIM"]
 
 MAX_NORM_DIM = 4096
 _DT = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16, torch.float32: _native.DTYPE_FP32}
@@ -107,6 +109,34 @@ def swiglu_gate_packed(gate_up: torch.Tensor) -> torch.Tensor:
     if gate_up.ndim < 1 or gate_up.shape[-1] % 16:
         raise ValueError("gate_up's last dim must be 2F with F a multiple of 8")
     return torch.ops.mega_trading_amd.swiglu_packed_fwd(gate_up)
+
+
+def apply_rope(
+    query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(rot(query), rot(key))`` (``triton_apply_rope``, ``triton_ops.py:45-54``).
+
+    ``query`` [B, Hq, T, D] and ``key`` [B, Hkv, T, D] (any strides), tables
+    [1, 1, >= T, D/2] as ``RotaryEmbedding`` keeps them (any float dtype, read
+    as fp32; rows past T are ignored).  Each interleaved pair (e, o) of row t
+    becomes (e cos - o sin, e sin + o cos) in fp32 with one rounding to the
+    input dtype; outputs have the inputs' layout.  The backward rotates the
+    gradients by -theta (``triton_ops.py:204-214``)."""
+    _check_device_dtype(query, "query")
+    if key.dtype != query.dtype or key.device != query.device:
+        raise RuntimeError("key must have the dtype and device of query")
+    if query.ndim != 4 or key.ndim != 4:
+        raise ValueError("query and key must be [B, H, T, D]")
+    b, _hq, t, d = query.shape
+    if key.shape[0] != b or key.shape[2] != t or key.shape[3] != d:
+        raise ValueError("key must be [B, Hkv, T, D] with the B, T and D of query")
+    if d % 2:
+        raise ValueError("RoPE requires an even head dimension")
+    c = _rope_table(cos, "cos", t, d, query.device)
+    s = _rope_table(sin, "sin", t, d, query.device)
+    if s.shape != c.shape:
+        raise ValueError("cos and sin must have the same shape")
+    return torch.ops.mega_trading_amd.rope_fwd(query, key, c, s, False)
 
 
 def fused_linear_cross_entropy(
@@ -196,6 +226,20 @@ def _weight(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     if w.dtype != x.dtype and w.dtype != torch.float32:
         w = w.to(torch.float32)
     return _flat(w)
+
+
+def _rope_table(table: torch.Tensor, name: str, t: int, d: int, device: torch.device) -> torch.Tensor:
+    """A [..., rows, D/2] table (leading dims of size 1) as fp32 [rows, D/2] with unit d stride."""
+    if table.ndim < 2 or any(n != 1 for n in table.shape[:-2]) or table.shape[-1] != d // 2:
+        raise ValueError(f"{name} must be [1, 1, T, D/2] with D/2 = {d // 2} (got {tuple(table.shape)})")
+    if table.shape[-2] < t:
+        raise ValueError(f"{name} has {table.shape[-2]} rows, fewer than the sequence length {t}")
+    if table.device != device:
+        raise RuntimeError(f"{name} must be on the device of query")
+    flat = table.reshape(table.shape[-2], table.shape[-1]).to(torch.float32)
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    return flat
 
 
 def _ptr_or_none(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -464,6 +508,28 @@ def _swiglu_packed_bwd_fake(gate_up, dout):
     return torch.empty_like(gate_up, memory_format=torch.contiguous_format)
 
 
+# Stand-alone RoPE of query and key in one launch; `inverse` rotates by
+# -theta (the backward).  Outputs take the inputs' layout (empty_like).
+@torch.library.custom_op("mega_trading_amd::rope_fwd", mutates_args=(), device_types="cuda")
+def rope_fwd(query: torch.Tensor, key: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, inverse: bool
+             ) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _native.load()
+    q_out, k_out = torch.empty_like(query), torch.empty_like(key)
+    b, hq, t, d = query.shape
+    strides = (ctypes.c_int64 * 16)(*query.stride(), *q_out.stride(), *key.stride(), *k_out.stride())
+    with torch.cuda.device(query.device):
+        rc = lib.mt_apply_rope(query.data_ptr(), key.data_ptr(), q_out.data_ptr(), k_out.data_ptr(), b, hq,
+                               key.shape[1], t, d, strides, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                               cos.shape[0], int(inverse), _DT[query.dtype], _stream(query))
+    _native.check(rc, "mt_apply_rope")
+    return q_out, k_out
+
+
+@rope_fwd.register_fake
+def _rope_fwd_fake(query, key, cos, sin, inverse):
+    return torch.empty_like(query), torch.empty_like(key)
+
+
 # Logits bytes per chunk.  Measured at the C5 shape (32768 x 16384 bf16 logits,
 # fwd + bwd): 64 MB chunks (cache-resident) 3.8 ms, 256 MB 2.7 ms, one 1 GB
 # chunk 2.3 ms (the three GEMMs alone take 1.6 ms), against 4.4 ms for the eager
@@ -626,6 +692,20 @@ def _swiglu_packed_backward(ctx, dout):
     return torch.ops.mega_trading_amd.swiglu_packed_bwd(gate_up, dout)
 
 
+def _rope_setup(ctx, inputs, output):
+    _q, _k, cos, sin, inverse = inputs
+    ctx.inverse = inverse
+    ctx.save_for_backward(cos, sin)
+
+
+def _rope_backward(ctx, dq, dk):
+    # a rotation's gradient is the opposite rotation (an unused output's
+    # gradient arrives as zeros: grads are materialized)
+    cos, sin = ctx.saved_tensors
+    gq, gk = torch.ops.mega_trading_amd.rope_fwd(dq, dk, cos, sin, not ctx.inverse)
+    return gq, gk, None, None, None
+
+
 def _ce_setup(ctx, inputs, output):
     _h, _w, _labels, _ignore, _dt, need_grad = inputs
     _loss, gh, gw = output
@@ -649,3 +729,4 @@ swiglu_fwd.register_autograd(_swiglu_backward, setup_context=_swiglu_setup)
 swiglu_packed_fwd.register_autograd(_swiglu_packed_backward, setup_context=_swiglu_packed_setup)
 rms_norm_fwd_mixed.register_autograd(_rms_mixed_backward, setup_context=_rms_mixed_setup)
 add_rms_norm_fwd_mixed.register_autograd(_add_rms_mixed_backward, setup_context=_add_rms_mixed_setup)
+rope_fwd.register_autograd(_rope_backward, setup_context=_rope_setup)

@@ -118,6 +118,17 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     assert lib.mt_rms_norm_bwd_mixed(p, p, p, None, p, p, None, p, p, need - 1, 1000, 512, BF16, FP32, None) == -6
     assert lib.mt_rms_norm_bwd_mixed(p, p, p, p + 4, p, p, None, p, p, need, 1000, 512, BF16, FP32, None) == -3
     assert lib.mt_rms_norm_fwd_mixed(p, 16, p, p, p, 0, 16, 1e-5, BF16, FP32, None) == 0
+    # stand-alone RoPE: even D, tables of at least T rows and D/2 wide, non-NULL operands
+    st = (ctypes.c_int64 * 16)(*([512, 64, 64, 1] * 4))
+    assert lib.mt_apply_rope(p, p, p, p, 1, 4, 2, 8, 7, st, p, p, 4, 8, 0, BF16, None) == -2
+    assert b"even head dimension" in lib.mt_last_error()
+    assert lib.mt_apply_rope(p, p, p, p, 1, 4, 2, 8, 64, st, p, p, 32, 7, 0, BF16, None) == -5  # 7 rows < T
+    assert lib.mt_apply_rope(p, p, p, p, 1, 4, 2, 8, 64, st, p, p, 16, 8, 0, BF16, None) == -5  # stride < D/2
+    assert lib.mt_apply_rope(p, p, p, p, 1, 4, 2, 8, 64, st, None, p, 32, 8, 0, BF16, None) == -1
+    assert lib.mt_apply_rope(p, None, p, p, 1, 4, 2, 8, 64, st, p, p, 32, 8, 0, BF16, None) == -1
+    assert lib.mt_apply_rope(p, p, p, p, 1, 4, 2, 8, 64, st, p, p, 32, 8, 0, 9, None) == -4
+    assert lib.mt_apply_rope(p, p, p, p, -1, 4, 2, 8, 64, st, p, p, 32, 8, 0, BF16, None) == -2
+    assert lib.mt_apply_rope(None, None, None, None, 0, 4, 2, 8, 64, None, None, None, 32, 8, 0, BF16, None) == 0
 
 
 def test_ops_reject_cpu_tensors(mta):
@@ -227,6 +238,29 @@ def test_validation_errors_on_device_tensors(mta):
             mta.rope_attention(q, k, k, cos, cos, repeats=2)
         with pytest.raises(ValueError, match="head_dim/2"):
             mta.rope_attention(q, k, k, torch.empty(8, 31, device="cuda"), torch.empty(8, 31, device="cuda"), repeats=2)
+
+
+def test_apply_rope_validation_like_the_reference_call(mta):
+    """ops.apply_rope (triton_apply_rope, triton_ops.py:45-54): [B, H, T, D]
+    query / key sharing B, T and D, even D, [1, 1, >= T, D/2] tables."""
+    with FakeTensorMode():
+        q, k = _fake((1, 4, 8, 64)), _fake((1, 2, 8, 64))
+        cs = torch.empty(1, 1, 16, 32, device="cuda")
+        qo, ko = mta.ops.apply_rope(q, k, cs, cs)
+        assert qo.shape == q.shape and ko.shape == k.shape
+        with pytest.raises(ValueError, match="even head dimension"):
+            mta.ops.apply_rope(_fake((1, 4, 8, 9)), _fake((1, 2, 8, 9)), cs, cs)
+        with pytest.raises(ValueError, match="B, T and D of query"):
+            mta.ops.apply_rope(q, _fake((1, 2, 9, 64)), cs, cs)
+        with pytest.raises(ValueError, match="fewer than the sequence length"):
+            mta.ops.apply_rope(q, k, cs[:, :, :4], cs[:, :, :4])
+        with pytest.raises(ValueError, match=r"D/2 = 32"):
+            mta.ops.apply_rope(q, k, torch.empty(1, 1, 16, 31, device="cuda"), cs)
+        with pytest.raises(RuntimeError, match="dtype and device of query"):
+            mta.ops.apply_rope(q, _fake((1, 2, 8, 64), torch.float16), cs, cs)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mta.ops.apply_rope(torch.zeros(1, 4, 8, 64), torch.zeros(1, 2, 8, 64), torch.zeros(1, 1, 8, 32),
+                           torch.zeros(1, 1, 8, 32))
 
 
 def test_fake_impls_give_shapes_for_tracing(mta):

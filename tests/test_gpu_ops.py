@@ -1,5 +1,6 @@
-"""GPU parity of the operator kernels (RMSNorm, add + RMSNorm, SwiGLU gate)
-against the CPU oracle (oracle/ops_oracle.py) and torch's eager routines.
+"""GPU parity of the operator kernels (RMSNorm, add + RMSNorm, SwiGLU gate,
+stand-alone RoPE) against the CPU oracle (oracle/ops_oracle.py,
+oracle/attention_oracle.py) and torch's eager routines.
 
 Tolerances: fp32 outputs rel 2e-5 (rsqrt and summation order), 16-bit outputs
 within one storage ulp of the oracle (RMSNorm) or value-for-value equal to it
@@ -15,6 +16,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from oracle import attention_oracle as ao
 from oracle import ops_oracle as oo
 
 pytestmark = pytest.mark.gpu
@@ -431,3 +433,97 @@ def test_tuned_gemm_replay_is_scoped_and_the_results_file_applies():
     assert (tun.is_enabled(), tun.tuning_is_enabled()) == before
     ref = a.double() @ w.double().t()
     assert ((y.double() - ref).norm() / ref.norm()).item() < 2 ** -8
+
+
+# ---------------------------------------------------------------------------
+# stand-alone RoPE (ops.apply_rope <- triton_apply_rope)
+# ---------------------------------------------------------------------------
+def _rope_layout(x, layout):
+    """A [B, H, T, D] tensor with x's values in the given memory layout."""
+    if layout == "bthd":  # the model's projection views
+        return x.transpose(1, 2).contiguous().transpose(1, 2)
+    if layout == "dstride2":  # every other element of a twice-as-wide buffer
+        wide = torch.zeros(*x.shape[:-1], 2 * x.shape[-1], dtype=x.dtype, device=x.device)
+        wide[..., ::2] = x
+        return wide[..., ::2]
+    return x
+
+
+def _check_rotation(got, x, cos, sin, dt, inverse=False):
+    """got == rot(x) (or rot^-1) from the fp64 oracle: one rounding to dt plus fp32 arithmetic error."""
+    xf = x.double().cpu().numpy()
+    c, s = cos.double().cpu().numpy(), sin.double().cpu().numpy()
+    ref = ao.rope_inverse(xf, c, s) if inverse else ao.apply_rope(xf, c, s)
+    pair = np.abs(xf[..., 0::2]) + np.abs(xf[..., 1::2])
+    mag = np.repeat(pair, 2, axis=-1)
+    tol = _ULP[dt] * np.abs(ref) + 2.0 ** -21 * mag
+    err = np.abs(got.double().cpu().numpy() - ref)
+    assert (err <= tol).all(), f"{(err > tol).sum()} values off; worst {err.max():.3e}"
+
+
+ROPE_CASES = [
+    # the reference's own parity shape (tests/test_training.py:627-647)
+    ((1, 16, 4, 512, 64), torch.bfloat16, "contig"),
+    ((2, 8, 2, 1024, 64), torch.bfloat16, "bthd"),    # the C5 layer's layout
+    ((1, 4, 2, 17, 128), torch.float16, "bthd"),
+    ((2, 4, 2, 33, 6), torch.float32, "contig"),      # D % 8 != 0: one pair per lane
+    ((1, 2, 1, 9, 8), torch.bfloat16, "dstride2"),    # d stride 2
+    ((1, 3, 3, 1, 32), torch.float32, "contig"),      # T = 1, R = 1
+]
+
+
+@pytest.mark.parametrize("shape,dt,layout", ROPE_CASES)
+def test_apply_rope_vs_oracle(mta, shape, dt, layout):
+    b, hq, hkv, t, d = shape
+    rope = mta.model.RotaryEmbedding(d, max(t, 8) + 5, theta=500_000.0).cuda()
+    q = _rope_layout(_gen((b, hq, t, d), 31, dt).cuda(), layout).requires_grad_(True)
+    k = _rope_layout(_gen((b, hkv, t, d), 32, dt).cuda(), layout).requires_grad_(True)
+    gq, gk = _gen((b, hq, t, d), 33, dt).cuda(), _gen((b, hkv, t, d), 34, dt).cuda()
+    # tables cast to the activation dtype and sliced to T, as RotaryEmbedding.forward passes them
+    cos = rope.cos[:, :, :t].to(dt)
+    sin = rope.sin[:, :, :t].to(dt)
+    qo, ko = mta.ops.apply_rope(q, k, cos, sin)
+    torch.autograd.backward((qo, ko), (gq, gk))
+    torch.cuda.synchronize()
+    assert qo.stride() == q.stride() or layout == "dstride2"
+    c2, s2 = cos[0, 0], sin[0, 0]
+    _check_rotation(qo.detach(), q.detach(), c2, s2, dt)
+    _check_rotation(ko.detach(), k.detach(), c2, s2, dt)
+    _check_rotation(q.grad, gq, c2, s2, dt, inverse=True)
+    _check_rotation(k.grad, gk, c2, s2, dt, inverse=True)
+
+
+def test_apply_rope_matches_the_torch_rotation_and_inverts(mta):
+    """Against the model's torch rotation (model.py:312-316) on fp32 tables,
+    and rot^-1(rot(x)) == x to fp32 rounding."""
+    rope = mta.model.RotaryEmbedding(64, 1024, theta=10_000.0).cuda()
+    q = _gen((2, 8, 1024, 64), 35, torch.float32).cuda()
+    k = _gen((2, 2, 1024, 64), 36, torch.float32).cuda()
+    qo, ko = mta.ops.apply_rope(q, k, rope.cos, rope.sin)
+    torch.testing.assert_close(qo, mta.model.rotate(q, rope.cos, rope.sin), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(ko, mta.model.rotate(k, rope.cos, rope.sin), rtol=1e-6, atol=1e-6)
+    back_q, back_k = torch.ops.mega_trading_amd.rope_fwd(qo, ko, rope.cos[0, 0], rope.sin[0, 0], True)
+    torch.testing.assert_close(back_q, q, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(back_k, k, rtol=1e-5, atol=1e-5)
+
+
+def test_rotary_embedding_hip_route_vs_torch_route(mta):
+    """RotaryEmbedding(operator_backend="triton") (model.py:292-293) against the
+    torch route on the same module tables, bf16, gradients included."""
+    hip = mta.model.RotaryEmbedding(64, 512, theta=500_000.0, operator_backend="triton").cuda()
+    ref = mta.model.RotaryEmbedding(64, 512, theta=500_000.0).cuda()
+    q = _gen((1, 16, 300, 64), 37, torch.bfloat16).cuda()
+    k = _gen((1, 4, 300, 64), 38, torch.bfloat16).cuda()
+    qa, ka = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+    qb, kb = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+    oa, pa = hip(qa, ka)
+    ob, pb = ref(qb, kb)
+    g1, g2 = torch.randn_like(oa), torch.randn_like(pa)
+    torch.autograd.backward((oa, pa), (g1, g2))
+    torch.autograd.backward((ob, pb), (g1, g2))
+    # the torch route rounds each product to bf16 before the sum; the kernel rounds
+    # once.  The reference's own bar for this comparison (tests/test_training.py:643-646)
+    for got, want in ((oa, ob), (pa, pb)):
+        torch.testing.assert_close(got.float(), want.float(), rtol=6e-2, atol=6e-2)
+    for got, want in ((qa.grad, qb.grad), (ka.grad, kb.grad)):
+        torch.testing.assert_close(got.float(), want.float(), rtol=8e-2, atol=8e-2)

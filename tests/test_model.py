@@ -15,6 +15,8 @@ import torch.nn.functional as F
 
 model_mod = importlib.import_module("mega-trading_amd.model")
 workload = importlib.import_module("mega-trading_amd.workload")
+RotaryEmbedding = model_mod.RotaryEmbedding
+rotate = model_mod.rotate
 
 
 def _attn(backend="auto", **kw):
@@ -45,15 +47,34 @@ def test_sdpa_route_uses_native_gqa():
 def test_hip_backend_calls_local_kernel(backend):
     attention = _attn(backend, fuse_rope=False)
     hidden = torch.randn(1, 8, 16)
-    with patch("mega-trading_amd.model._hip_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
+    # the RoPE kernel stand-in rotates in torch, so the attention sees rotated q / k
+    with patch("mega-trading_amd.model._hip_apply_rope",
+               side_effect=lambda q, k, c, s: (rotate(q, c, s), rotate(k, c, s))) as rope_op, \
+            patch("mega-trading_amd.model._hip_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
         out = attention(hidden)
+    rope_op.assert_called_once()
     query, key, value = op.call_args.args[:3]
     assert out.shape == hidden.shape
     assert query.shape == (1, 4, 8, 4) and key.shape[1] == 2 and value.shape[1] == 2
     assert op.call_args.kwargs["repeats"] == 2
-    # RoPE was applied in torch before the call, as model.py:223 does
+    # RoPE was applied before the call, as model.py:223 does
     raw_q = attention.q_proj(hidden).view(1, 8, 4, 4).transpose(1, 2)
-    assert torch.allclose(query, attention.rope(raw_q, raw_q)[0])
+    cos, sin = attention.rope.cos[:, :, :8], attention.rope.sin[:, :, :8]
+    assert torch.allclose(query, rotate(raw_q, cos, sin))
+
+
+@pytest.mark.parametrize("backend,kernel", [("triton", True), ("hip", True), ("auto", False), ("math", False)])
+def test_rotary_embedding_routes_by_operator_backend(backend, kernel):
+    # as the reference test patches _triton_apply_rope (tests/test_training.py:470-475)
+    rope = RotaryEmbedding(head_dim=4, max_sequence_length=8, theta=10_000.0, operator_backend=backend)
+    query, key = torch.randn(1, 4, 8, 4), torch.randn(1, 2, 8, 4)
+    with patch("mega-trading_amd.model._hip_apply_rope", return_value=(query, key)) as rope_kernel:
+        out_q, _out_k = rope(query, key)
+    assert rope_kernel.call_count == (1 if kernel else 0)
+    assert out_q.shape == query.shape
+    if kernel:
+        _q, _k, cos, sin = rope_kernel.call_args.args
+        assert cos.shape == (1, 1, 8, 2) and cos.dtype == query.dtype  # cast as model.py:290-291
 
 
 def test_fused_rope_route_passes_fp32_tables_and_raw_qk():
@@ -98,10 +119,12 @@ def test_dropout_in_training_falls_back_to_sdpa():
     attention.train()
     hidden = torch.randn(1, 8, 16)
     with patch("mega-trading_amd.model.F.scaled_dot_product_attention", return_value=torch.zeros(1, 4, 8, 4)) as sdpa, \
-            patch("mega-trading_amd.model._hip_rope_attention") as op:
+            patch("mega-trading_amd.model._hip_rope_attention") as op, \
+            patch("mega-trading_amd.model._hip_apply_rope", side_effect=lambda q, k, c, s: (q, k)) as rope_op:
         attention(hidden)
     assert sdpa.call_args.kwargs["dropout_p"] == 0.1
     op.assert_not_called()
+    rope_op.assert_called_once()  # the RoPE still takes the backend (model.py:213, 223)
     attention.eval()
     with patch("mega-trading_amd.model._hip_rope_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
         attention(hidden)
