@@ -348,9 +348,16 @@ def cpu_model_name() -> str:
 
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = {}
         for line in out.splitlines():
-            if line.strip().startswith("Model name:"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, val = line.split(":", 1)
+                fields.setdefault(key.strip(), val.strip())
+        if "Model name" in fields:
+            # a virtualised host may report only the product family: add lscpu's
+            # family / model / stepping numbers, which identify the part
+            ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if k in fields]
+            return fields["Model name"] + (f" ({', '.join(ids)})" if ids else "")
     except (OSError, subprocess.SubprocessError):
         pass
     try:

@@ -31,6 +31,9 @@
 //     LDS once for all 4 waves.  The group's heads may be split over several
 //     workgroups (fp32 partial sums, combined by attn_bwd_combine_kernel) so
 //     the causal triangle spreads over enough workgroups to balance.
+//   * Backward launches: a prep pass writes -delta and -LSE log2(e) per query
+//     row; at D <= 64 the dQ and dK/dV workgroups then share one grid
+//     (attn_bwd_kernel), at D = 128 they are two launches.
 // Fully masked causal tiles are never visited; only diagonal tiles mask.
 #pragma once
 
@@ -53,8 +56,8 @@ struct AttnParams {
   uint16_t* dk;
   uint16_t* dv;
   float* lse;      // [B, Hq, T] natural-log LSE (written by fwd, read by bwd)
-  float* ndelta;   // [B, Hq, T] -rowsum(O * dO) workspace (written by dQ, read by dK/dV)
-  float* nlse2;    // [B, Hq, T] -LSE * log2(e) workspace (written by dQ, read by dK/dV)
+  float* ndelta;   // [B, Hq, T] -rowsum(O * dO) workspace (written by the prep pass, read by dQ and dK/dV)
+  float* nlse2;    // [B, Hq, T] -LSE * log2(e) workspace (written by the prep pass, read by dQ and dK/dV)
   float* part;     // [n_split, 2, B, Hkv, T, D] fp32 dK/dV partial sums (bwd, n_split > 1)
   const float* cos;  // [T, D/2] fp32 or null
   const float* sin;
@@ -678,7 +681,7 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
 }
 
 // ===========================================================================
-// Backward, dQ (also writes delta = rowsum(O * dO))
+// Backward, dQ
 // ===========================================================================
 // One 64-key K/V tile against the wave's 64 query rows: S^T and dP^T
 // recomputed (lane = query), P = 2^(S c2 - lse2), dS = P (dP - delta),
