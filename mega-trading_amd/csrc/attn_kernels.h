@@ -72,6 +72,7 @@ struct AttnParams {
   int nkb;        // dK/dV: key blocks
   int n_kv_tasks; // attn_bwd_kernel: dK/dV workgroups in the grid
   int n_dq_tasks; // attn_bwd_kernel: dQ workgroups in the grid
+  int fwd_fold;   // forward grids of one resident round: workgroups past this index run in reverse order (0: off)
   float scale;       // softmax scale (1/sqrt(D) by default)
   float scale_log2;  // scale * log2(e)
 };
@@ -130,6 +131,21 @@ __device__ __forceinline__ RowTask row_task(const AttnParams& p, int L) {
   t.kvh = bk % p.Hkv;
   t.b = bk / p.Hkv;
   return t;
+}
+
+// A forward grid that fits one resident round (at most two workgroups per CU)
+// gets no dynamic balancing: every workgroup starts at once, and a CU's time
+// is the sum of its two workgroups' causal lengths.  The first `fold`
+// workgroups (one per CU) keep the heaviest-first order; the rest run in
+// reverse, lightest first, so the workgroup that shares a CU with the k-th
+// heaviest is the k-th lightest and every CU gets about the same work.  The
+// reversal moves whole chunks of 8 workgroups, so a workgroup keeps its XCD
+// (index mod 8).
+__device__ __forceinline__ int fold_order(int L, int n, int fold) {
+  if (fold == 0 || L < fold) return L;
+  const int m = n - fold, j = L - fold;
+  if (((m | fold) & 7) == 0) return fold + (m - 8 - (j & ~7)) + (j & 7);
+  return fold + (m - 1 - j);
 }
 
 // ===========================================================================
@@ -337,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
   // [buf][K, V] x 128 rows (two 64-row tiles back to back)
   __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];
 
-  const RowTask task = row_task(p, blockIdx.x);
+  const RowTask task = row_task(p, fold_order(blockIdx.x, gridDim.x, p.fwd_fold));
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -985,13 +1001,15 @@ __device__ __forceinline__ void dq32_tile(const char* K, const char* Vr, const t
   }
 }
 
-template <class E, int D, bool ROPE, bool PEEL>
-__global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_bwd_dq_w8_kernel(AttnParams p) {
+// NW waves per workgroup: the RowTask's NW / 2 (head, row block) pairs
+// (the launch sets r_sub and rb for that many pairs).
+template <class E, int D, bool ROPE, bool PEEL, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void attn_bwd_dq_w8_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  constexpr int SW = TL::INSTR < kFwdW8Waves ? TL::INSTR : kFwdW8Waves;  // waves that stage tiles
+  constexpr int SW = TL::INSTR < NW ? TL::INSTR : NW;  // waves that stage tiles
   __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buf][K, V]
 
   const RowTask task = row_task(p, blockIdx.x);

@@ -147,6 +147,25 @@ size_t workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
   return workspace_bytes_split(B, Hq, Hkv, T, D, choose_split(B, Hq, Hkv, T, D));
 }
 
+// fwd / dQ workgroup geometry for `pairs` (query head, 64-row block) pairs per
+// workgroup: the heads of a KV group first (r_sub of them), then row blocks.
+void set_pairs(mt::AttnParams& p, int pairs) {
+  p.r_sub = (p.R % pairs == 0) ? pairs : (pairs >= 2 && p.R % 2 == 0) ? 2 : 1;
+  p.n_hsub = p.R / p.r_sub;
+  p.rb = pairs / p.r_sub;
+  p.nsb = (p.nqb + p.rb - 1) / p.rb;
+}
+
+// Waves per D = 128 dQ workgroup: 8 (one workgroup per CU) or 4 (two per
+// CU, each barrier then stalls only half of a CU's waves).  Measured at
+// BASELINE config 4 (A/B on one box): 4 waves take the dQ kernel from 0.465
+// to 0.433 ms, but the whole fwd+bwd step stays at 1.51 ms (the dK/dV kernel
+// that follows runs correspondingly slower), so 8 is kept.
+#ifndef MT_DQ128_WAVES
+#define MT_DQ128_WAVES 8
+#endif
+constexpr int kDq128Waves = MT_DQ128_WAVES;
+
 // split = 0: the dK/dV head split of choose_split; else that split (a divisor of R)
 void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, float scale, int split = 0) {
   p.B = B;
@@ -154,11 +173,8 @@ void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, floa
   p.Hkv = Hkv;
   p.T = T;
   p.R = Hq / Hkv;
-  p.r_sub = (p.R % 4 == 0) ? 4 : (p.R % 2 == 0) ? 2 : 1;
-  p.n_hsub = p.R / p.r_sub;
-  p.rb = 4 / p.r_sub;
   p.nqb = (T + mt::kBlk - 1) / mt::kBlk;
-  p.nsb = (p.nqb + p.rb - 1) / p.rb;
+  set_pairs(p, 4);
   p.nkb = (T + kv_keys(D) - 1) / kv_keys(D);
   p.n_split = split > 0 ? split : choose_split(B, Hq, Hkv, T, D);
   p.scale = scale;
@@ -186,6 +202,13 @@ hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
     p.sk[2] = D;
   }
   dim3 grid(p.nsb * p.B * p.Hkv * p.n_hsub);
+#ifndef MT_FWD_FOLD
+#define MT_FWD_FOLD 1
+#endif
+  // one resident round (more than one and at most two workgroups per CU):
+  // pair heavy and light row blocks on each CU
+  const int cus = device_cus();
+  p.fwd_fold = (MT_FWD_FOLD && (int)grid.x > cus && (int)grid.x <= 2 * cus) ? cus : 0;
   if constexpr (D > 64) {
     const dim3 block(64 * mt::kFwdW8Waves);
     return p.rb == 1 ? launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, true>, grid, block, st, p)
@@ -219,9 +242,13 @@ hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
     if (e != hipSuccess) return e;
   } else {
     if (stage & 1) {
-      const dim3 block(64 * mt::kFwdW8Waves);
-      hipError_t e = p.rb == 1 ? launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, true>, dim3(n_dq), block, st, p)
-                               : launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, false>, dim3(n_dq), block, st, p);
+      // kDq128Waves waves per workgroup: kDq128Waves / 2 (head, row block) pairs
+      mt::AttnParams pq = p;
+      set_pairs(pq, kDq128Waves / 2);
+      const dim3 grid(pq.nsb * pq.B * pq.Hkv * pq.n_hsub), block(64 * kDq128Waves);
+      hipError_t e = pq.rb == 1
+                         ? launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, true, kDq128Waves>, grid, block, st, pq)
+                         : launch_main(mt::attn_bwd_dq_w8_kernel<E, D, ROPE, false, kDq128Waves>, grid, block, st, pq);
       if (e != hipSuccess) return e;
     }
     if (stage & 2) {
