@@ -953,7 +953,9 @@ __device__ __forceinline__ void dq_body(const AttnParams& p, int L, char* lds) {
 // As for the D = 128 forward: the 4 (head, 64-row block) pairs of a RowTask
 // split into two 32-row waves, two waves per SIMD and no spills.  At D = 128
 // attn_bwd_dq_kernel re-reads the K / V operands for each 32-query half
-// anyway, so the narrower wave costs no extra LDS reads per MFMA.
+// anyway, so the narrower wave costs no extra LDS reads per MFMA.  It runs
+// before the dK/dV pass (separate launches) and writes the -delta and
+// -LSE log2(e) vectors that pass reads.
 template <class E, int D, bool MASK>
 __device__ __forceinline__ void dq32_tile(const char* K, const char* Vr, const typename E::v8* qop,
                                           const typename E::v8* gop, f32x16* dqacc, float lse2, float dlt, int rbase,
@@ -1031,28 +1033,45 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_bwd_dq_w8_kernel(AttnParams p
   const int64_t rowbase = ((int64_t)task.b * p.Hq + head) * p.T;
 
   V8 qop[KT], gop[KT];
-  float lse2, dlt;  // LSE log2(e) and delta of the lane's row (from attn_bwd_prep_kernel)
+  float lse2, dlt;  // LSE log2(e) and delta of the lane's row
   {
+    // This kernel is the D = 128 backward's first pass, so it computes the
+    // row's delta = rowsum(O * dO) in fp32 itself (the lane and its lane^32
+    // partner hold the two halves of the row) and stores -delta and
+    // -LSE log2(e) for the dK/dV pass; no separate prep pass.
     const uint16_t* qbase = p.q + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     const uint16_t* gbase = p.dout + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
+    const uint16_t* obase = p.o + task.b * p.so[0] + (int64_t)head * p.so[1];
     const int row = q0 + l32;
     const int rc = min(row, p.T - 1);
     const bool ok = active && row < p.T;
-    u32x4 qx[KT], gx[KT];
+    u32x4 qx[KT], gx[KT], ox[KT];
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
       const int d0 = 16 * kk + 8 * hh;
       qx[kk] = *reinterpret_cast<const u32x4*>(qbase + (int64_t)rc * p.sq[2] + d0);
       gx[kk] = *reinterpret_cast<const u32x4*>(gbase + (int64_t)rc * p.sdo[2] + d0);
+      ox[kk] = *reinterpret_cast<const u32x4*>(obase + (int64_t)rc * p.so[2] + d0);
     }
-    const float nl = p.nlse2[rowbase + rc], nd = p.ndelta[rowbase + rc];
+    const float lse = p.lse[rowbase + rc];
+    float part = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        part += lo_f<E>(gx[kk][w]) * lo_f<E>(ox[kk][w]) + hi_f<E>(gx[kk][w]) * hi_f<E>(ox[kk][w]);
+    const float delta = sum_with_partner(part);
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
       qop[kk] = __builtin_bit_cast(V8, ok ? qx[kk] : zero4());
       gop[kk] = __builtin_bit_cast(V8, ok ? gx[kk] : zero4());
     }
-    dlt = ok ? -nd : 0.f;
-    lse2 = ok ? -nl : 0.f;
+    dlt = ok ? delta : 0.f;
+    lse2 = ok ? lse * kLog2e : 0.f;
+    if (ok && hh == 0) {
+      p.ndelta[rowbase + row] = -delta;
+      p.nlse2[rowbase + row] = -lse * kLog2e;
+    }
   }
 
   f32x16 dqacc[DT];

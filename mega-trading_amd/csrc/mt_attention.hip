@@ -224,7 +224,9 @@ template <class E, int D, bool ROPE>
 hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
   const int n_dq = p.nsb * p.B * p.Hkv * p.n_hsub;
   const int n_kv = p.nkb * p.B * p.Hkv * p.n_split;
-  if (stage & 1) {
+  if (D <= 64 && (stage & 1)) {
+    // -delta and -LSE log2(e) for both kinds of task (at D = 128 the dQ
+    // kernel, which runs first, writes them)
     const int64_t rows = (int64_t)p.B * p.Hq * p.T;
     const int64_t rows_per_block = 256 / (D / 8);
     hipLaunchKernelGGL((mt::attn_bwd_prep_kernel<E, D>), dim3((unsigned)((rows + rows_per_block - 1) / rows_per_block)),
