@@ -57,6 +57,26 @@ def test_baseline_config_parity(mta, name, rope):
         print(name, "rope" if rope else "plain", (bi, g), {k_: f"{v_:.2e}" for k_, v_ in errs.items()}, flush=True)
 
 
+@pytest.mark.parametrize("b,hkv,t", [(9, 2, 960), (10, 2, 960), (16, 2, 1024)])
+def test_one_round_forward_grids(mta, b, hkv, t):
+    """Forward grids of one resident round (256 < workgroups <= 512 on the
+    MI355X's 256 CUs) run their second half lightest first: 270 and 300
+    workgroups (the tail reversed workgroup by workgroup) and BASELINE
+    config 2's 512 (reversed in chunks of 8).  Every row of the forward is
+    checked against the oracle, so a task left out or run twice shows; the
+    backward on the first and the last (batch, group) slice."""
+    hq, d = 4 * hkv, 64
+    q, k, v, do = make_inputs(b, t, hq, hkv, d, sigma=0.5, seed=b * 31 + t)
+    got = run_hip(mta, q, k, v, do, 4)
+    o_ref, lse_ref = orc.attention_forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), 4)
+    assert np.abs(got[0] - o_ref).max() <= TOL_OUT_MAXABS
+    assert np.abs(got[1] - lse_ref).max() <= 1e-2
+    for bi, g in ((0, 0), (b - 1, hkv - 1)):
+        hs = slice(g * 4, (g + 1) * 4)
+        ref = oracle(q[bi : bi + 1, hs], k[bi : bi + 1, g : g + 1], v[bi : bi + 1, g : g + 1], do[bi : bi + 1, hs], 4)
+        compare(slice_group(got, bi, g, 4), ref)
+
+
 @pytest.mark.parametrize("t", [1, 2, 17, 63, 64, 65, 127, 200, 333])
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (4, 2), (8, 2), (16, 2), (6, 2)])
 def test_ragged_lengths_and_group_sizes(mta, t, hq, hkv):
