@@ -205,6 +205,43 @@ def test_packed_qkv_equals_the_head_views(mta, b, t, hq, hkv, d, dt):
     assert torch.equal(dq, q.grad) and torch.equal(dk, k.grad) and torch.equal(dv, v.grad)
 
 
+@pytest.mark.parametrize("t,rope", [(16384, False), (12345, True)])
+def test_long_sequences_against_fp32_torch(mta, t, rope):
+    """T four times BASELINE config 3's (and a ragged one): row indices, tile
+    offsets and the causal loops at lengths the oracle is too slow for,
+    against a float32 torch reference on the GPU (the dense softmax
+    formula; the group's K/V repeated per query head).  BASELINE tolerances."""
+    b, hq, hkv, d = 1, 4, 1, 64
+    q, k, v, do = make_inputs(b, t, hq, hkv, d, sigma=0.5, seed=t)
+    cos = sin = None
+    if rope:
+        cos, sin = orc.rope_tables(t, d, 10_000.0)
+    got = run_hip(mta, q, k, v, do, hq // hkv, cos, sin)
+    dev = torch.device("cuda:0")
+    qf, kf, vf = (x.float().to(dev).requires_grad_(True) for x in (q, k, v))
+    qr, kr = qf, kf
+    if rope:
+        c = torch.from_numpy(cos).to(dev)
+        s_ = torch.from_numpy(sin).to(dev)
+
+        def rot(x):
+            e, o = x[..., 0::2], x[..., 1::2]
+            return torch.stack((e * c - o * s_, e * s_ + o * c), dim=-1).flatten(-2)
+
+        qr, kr = rot(qf), rot(kf)
+    kk = kr.repeat_interleave(hq // hkv, dim=1)
+    vv = vf.repeat_interleave(hq // hkv, dim=1)
+    scores = torch.matmul(qr, kk.transpose(-2, -1).contiguous()) / d ** 0.5
+    mask = torch.ones(t, t, dtype=torch.bool, device=dev).triu(1)
+    scores = scores.masked_fill(mask, float("-inf"))
+    lse = torch.logsumexp(scores, dim=-1)
+    out = torch.matmul(torch.softmax(scores, dim=-1), vv)
+    dq, dk, dv = torch.autograd.grad(out, (qf, kf, vf), do.float().to(dev))
+    f = lambda x: x.detach().float().cpu().numpy()  # noqa: E731
+    errs = compare(got, (f(out), f(lse), f(dq), f(dk), f(dv)))
+    print(t, "rope" if rope else "plain", {k_: f"{v_:.2e}" for k_, v_ in errs.items()}, flush=True)
+
+
 def test_causality_and_determinism_at_full_size(mta):
     """C3 shape: changing keys/values at positions >= t0 leaves output rows < t0
     bit-identical, and repeated runs are bit-identical (no atomics anywhere)."""
