@@ -93,6 +93,14 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// sigmoid(g) = 1 / (1 + e^-g) from the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32, about 1 ulp each) rather than the correctly rounded
+// library sequences, which made the SwiGLU kernels issue-bound; e^-g = inf
+// gives 0 and e^-g = 0 gives 1, as the exact formula does.
+__device__ __forceinline__ float sigmoid_fast(float g) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e));
+}
+
 // ===========================================================================
 // RMSNorm forward (ADD: the residual add fused in front)
 //   ADD:  s = x + r (fp32), new_res = s (stored in ST), y = s * rstd * w
@@ -323,7 +331,7 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const void* gate, const
       if (i < nvec) {
         float o[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[q][j] / (1.f + expf(-g[q][j]))) * u[q][j];
+        for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[q][j] * sigmoid_fast(g[q][j])) * u[q][j];
         IO<DT>::store8(out, 8 * i, o);
       }
     }
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const void* gate, const
   const int64_t t = 8 * nvec + (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t < n && (int64_t)blockIdx.x * 256 + threadIdx.x < 8) {
     const float g = IO<DT>::load1(gate, t);
-    IO<DT>::store1(out, t, IO<DT>::round(g / (1.f + expf(-g))) * IO<DT>::load1(up, t));
+    IO<DT>::store1(out, t, IO<DT>::round(g * sigmoid_fast(g)) * IO<DT>::load1(up, t));
   }
 }
 
@@ -358,11 +366,10 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const
         float dg[8], du[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float e = expf(-g[q][j]);
-          const float sg = 1.f / (1.f + e);
+          const float sg = sigmoid_fast(g[q][j]);
           const float t = IO<DT>::round(dy[q][j] * u[q][j]);
           dg[j] = (t * sg) * (1.f + g[q][j] * (1.f - sg));
-          du[j] = dy[q][j] * IO<DT>::round(g[q][j] / (1.f + e));
+          du[j] = dy[q][j] * IO<DT>::round(g[q][j] * sg);
         }
         IO<DT>::store8(dgate, 8 * i, dg);
         IO<DT>::store8(dup, 8 * i, du);
@@ -372,10 +379,9 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const void* gate, const
   const int64_t t = 8 * nvec + (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t < n && (int64_t)blockIdx.x * 256 + threadIdx.x < 8) {
     const float g = IO<DT>::load1(gate, t), u = IO<DT>::load1(up, t), dy = IO<DT>::load1(dout, t);
-    const float e = expf(-g);
-    const float sg = 1.f / (1.f + e);
+    const float sg = sigmoid_fast(g);
     IO<DT>::store1(dgate, t, (IO<DT>::round(dy * u) * sg) * (1.f + g * (1.f - sg)));
-    IO<DT>::store1(dup, t, dy * IO<DT>::round(g / (1.f + e)));
+    IO<DT>::store1(dup, t, dy * IO<DT>::round(g * sg));
   }
 }
 
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(256) void swiglu_packed_fwd_kernel(const void* gu, 
     IO<DT>::load8(gu, g0, g);
     IO<DT>::load8(gu, g0 + 8 * cpr, u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[j] / (1.f + expf(-g[j]))) * u[j];
+    for (int j = 0; j < 8; ++j) o[j] = IO<DT>::round(g[j] * sigmoid_fast(g[j])) * u[j];
     IO<DT>::store8(out, 8 * (int64_t)i, o);
   }
 }
@@ -412,11 +418,10 @@ __global__ __launch_bounds__(256) void swiglu_packed_bwd_kernel(const void* gu, 
     IO<DT>::load8(dout, 8 * (int64_t)i, dy);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float e = expf(-g[j]);
-      const float sg = 1.f / (1.f + e);
+      const float sg = sigmoid_fast(g[j]);
       const float t = IO<DT>::round(dy[j] * u[j]);
       dg[j] = (t * sg) * (1.f + g[j] * (1.f - sg));
-      du[j] = dy[j] * IO<DT>::round(g[j] / (1.f + e));
+      du[j] = dy[j] * IO<DT>::round(g[j] * sg);
     }
     IO<DT>::store8(dgu, g0, dg);
     IO<DT>::store8(dgu, g0 + 8 * cpr, du);
