@@ -212,6 +212,15 @@ def time_ops(pkg, iters=20):
     loss_rows = torch.empty(rows, device=dev)
     f32, bf16 = native.DTYPE_FP32, native.DTYPE_BF16
     mb = lambda n_elems, elem: n_elems * elem  # noqa: E731
+    # stand-alone RoPE of one C5 layer's q [32, 8, 1024, 64] and k [32, 2, 1024, 64] in the
+    # projection layout ([B, T, H, D] memory, the model's views), tables [1024, 32] fp32
+    hq, hkv, hd, tt = 8, 2, 64, 1024
+    rq = torch.randn(32, tt, hq, hd, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+    rk = torch.randn(32, tt, hkv, hd, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+    rqo, rko = torch.empty_like(rq), torch.empty_like(rk)
+    rcos = torch.randn(tt, hd // 2, device=dev, generator=g)
+    rsin = torch.randn(tt, hd // 2, device=dev, generator=g)
+    rst = (ctypes.c_int64 * 16)(*rq.stride(), *rqo.stride(), *rk.stride(), *rko.stride())
     cases = {
         "rms_norm_fwd (fp32 32768x512)": (
             lambda: lib.mt_rms_norm_fwd(x.data_ptr(), hid, w.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, hid,
@@ -228,6 +237,10 @@ def time_ops(pkg, iters=20):
             lambda: lib.mt_swiglu_bwd(gate.data_ptr(), up.data_ptr(), dout.data_ptr(), dgate.data_ptr(),
                                       dup.data_ptr(), gate.numel(), bf16, sp),
             5 * mb(gate.numel(), 2)),
+        "apply_rope (bf16 q 32x8x1024x64 + k 32x2x1024x64)": (
+            lambda: lib.mt_apply_rope(rq.data_ptr(), rk.data_ptr(), rqo.data_ptr(), rko.data_ptr(), 32, hq, hkv, tt,
+                                      hd, rst, rcos.data_ptr(), rsin.data_ptr(), hd // 2, tt, 0, bf16, sp),
+            2 * mb(rq.numel() + rk.numel(), 2) + 2 * mb(rcos.numel(), 4)),
         "cross_entropy_rows (bf16 32768x16384, grad in place)": (
             lambda: lib.mt_cross_entropy_rows(logits.data_ptr(), vocab, labels.data_ptr(), rows, vocab,
                                               n_valid.data_ptr(), -100, loss_rows.data_ptr(), 1, bf16, sp),

@@ -231,8 +231,13 @@ int rms_bwd_common(const void* s, const void* w, const float* rstd, const void* 
 namespace {
 template <int DT>
 void rope_launch(bool vec, dim3 grid, hipStream_t st, const K::RopeArgs& a) {
-  if (vec) hipLaunchKernelGGL((K::rope_kernel<DT, true>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((K::rope_kernel<DT, false>), grid, dim3(256), 0, st, a);
+  if (a.n + 256 < (int64_t(1) << 32)) {
+    if (vec) hipLaunchKernelGGL((K::rope_kernel<DT, true, uint32_t>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((K::rope_kernel<DT, false, uint32_t>), grid, dim3(256), 0, st, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((K::rope_kernel<DT, true, int64_t>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((K::rope_kernel<DT, false, int64_t>), grid, dim3(256), 0, st, a);
+  }
 }
 }  // namespace
 

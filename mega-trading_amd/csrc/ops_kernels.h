@@ -580,20 +580,35 @@ struct RopeArgs {
   int64_t n;           // lane units of q and k
 };
 
-template <int DT, bool VEC>
+// I: the index type of the (unit -> b, h, t, pair) decomposition; uint32_t
+// whenever the unit count allows (64-bit divisions are long instruction
+// sequences).  Rows are visited in memory order: (b, h, t) for [B, H, T, D]
+// storage, (b, t, h) when the heads are interleaved per token (the model's
+// projection views, [B, T, H, D] storage).
+template <int DT, bool VEC, class I>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
-  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (u >= a.n) return;
-  const int w = u >= a.n0 ? 1 : 0;
-  const int64_t local = u - (w ? a.n0 : 0);
+  const I u = (I)blockIdx.x * 256 + threadIdx.x;
+  if ((int64_t)u >= a.n) return;
+  const int w = (int64_t)u >= a.n0 ? 1 : 0;
+  const I local = u - (w ? (I)a.n0 : (I)0);
   constexpr int P = VEC ? 4 : 1;  // pairs per lane
-  const int per_row = a.half / P;
+  const I per_row = (I)(a.half / P);
   const int i = int(local % per_row) * P;  // first pair
-  const int64_t row = local / per_row;
-  const int t = int(row % a.T);
-  const int64_t bh = row / a.T;
-  const int h = int(bh % a.heads[w]);
-  const int64_t b = bh / a.heads[w];
+  const I row = local / per_row;
+  int t, h;
+  I bq;
+  if (a.ss[w][1] <= a.ss[w][2]) {  // heads inside tokens: row = (b T + t) H + h
+    h = int(row % (I)a.heads[w]);
+    const I bt = row / (I)a.heads[w];
+    t = int(bt % (I)a.T);
+    bq = bt / (I)a.T;
+  } else {  // row = (b H + h) T + t
+    t = int(row % (I)a.T);
+    const I bh = row / (I)a.T;
+    h = int(bh % (I)a.heads[w]);
+    bq = bh / (I)a.heads[w];
+  }
+  const int64_t b = (int64_t)bq;
   const int64_t so = b * a.ss[w][0] + h * a.ss[w][1] + t * a.ss[w][2];
   const int64_t dO = b * a.sd[w][0] + h * a.sd[w][1] + t * a.sd[w][2];
   const float* cp = a.cos + t * a.tstride + i;
