@@ -485,7 +485,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
 // attn_fwd_kernel (fp32 scale and offset per score, lazy rescaling).
 constexpr int kFwdW8Waves = 8;
 
-template <class E, int D, bool MASK>
+// NQ 32-key quarters per staged tile (4: 128 keys, 2: 64 keys).
+template <class E, int D, bool MASK, int NQ = 4>
 __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const typename E::v8* qop, f32x16* oacc,
                                            float& mrun, float& lrun, int rbase, TrBase tbase, int lane, int kt0,
                                            int q0, float c2) {
@@ -495,9 +496,9 @@ __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const 
   constexpr int DT = D / 32;
   const int hh = lane >> 5;
   const int l32 = lane & 31;
-  bool live[4];
+  bool live[NQ];
 #pragma unroll
-  for (int h = 0; h < 4; ++h) live[h] = !MASK || (kt0 + 32 * h <= q0 + 31);
+  for (int h = 0; h < NQ; ++h) live[h] = !MASK || (kt0 + 32 * h <= q0 + 31);
 
   auto sq = [&](int h, f32x16& st) {
     const char* Kh = K + (h >> 1) * TL::BYTES;
@@ -565,8 +566,8 @@ __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const 
   V8 pk[2];
   if (live[0]) sq(0, st[0]);
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    if (h < 3 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
+  for (int h = 0; h < NQ; ++h) {
+    if (h < NQ - 1 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
     float qs = 0.f;
     if (live[h]) qs = ex(h, st[h & 1], pk);
     __builtin_amdgcn_sched_barrier(0);
@@ -578,14 +579,17 @@ __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const 
   }
 }
 
-template <class E, int D, bool ROPE, bool PEEL>
-__global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnParams p) {
+// NW waves per workgroup (the RowTask's NW / 2 (head, row block) pairs; the
+// launch sets r_sub and rb for that many), KEYS keys per staged K / V tile.
+template <class E, int D, bool ROPE, bool PEEL, int NW = kFwdW8Waves, int KEYS = kFwdKeys>
+__global__ __launch_bounds__(64 * NW, 2) void attn_fwd_w8_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
-  constexpr int SW = TL::INSTR < kFwdW8Waves ? TL::INSTR : kFwdW8Waves;  // waves that stage tiles
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][2 * TL::BYTES];  // [buf][K, V] x 128 rows
+  constexpr int NQ = KEYS / 32;
+  constexpr int SW = TL::INSTR < NW ? TL::INSTR : NW;  // waves that stage tiles
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][(KEYS / 64) * TL::BYTES];  // [buf][K, V] x KEYS rows
 
   const RowTask task = row_task(p, blockIdx.x);
   const int tid = threadIdx.x;
@@ -598,9 +602,9 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
   const int qb = task.sb * p.rb + pw / p.r_sub;     // this wave's row block
   const int q0 = qb * kBlk + 32 * (wave & 1);       // this wave's first row
   const bool active = qb < p.nqb && q0 < p.T;
-  const int jw = (q0 + 31) / kFwdKeys;              // this wave's diagonal tile
+  const int jw = (q0 + 31) / KEYS;                  // this wave's diagonal tile
   const int last_row = min(p.T, (task.sb * p.rb + p.rb) * kBlk) - 1;
-  const int jlast = last_row / kFwdKeys;
+  const int jlast = last_row / KEYS;
 
   const uint16_t* kbase = p.k + task.b * p.sk[0] + (int64_t)task.kvh * p.sk[1];
   const uint16_t* vbase = p.v + task.b * p.sv[0] + (int64_t)task.kvh * p.sv[1];
@@ -649,11 +653,13 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
   const TrBase tbase_op = TL::tr_base(lane);
   auto stage = [&](int j, int buf) {
     if (!stager) return;
-    const int r0 = j * kFwdKeys;
+    const int r0 = j * KEYS;
     ks_stage.stage(smem[buf][0], kbase, p.sk[2], r0, p.T);
     vs_stage.stage(smem[buf][1], vbase, p.sv[2], r0, p.T);
-    ks_stage.stage(smem[buf][0] + TL::BYTES, kbase, p.sk[2], r0 + kBlk, p.T);
-    vs_stage.stage(smem[buf][1] + TL::BYTES, vbase, p.sv[2], r0 + kBlk, p.T);
+    if constexpr (KEYS == 128) {
+      ks_stage.stage(smem[buf][0] + TL::BYTES, kbase, p.sk[2], r0 + kBlk, p.T);
+      vs_stage.stage(smem[buf][1] + TL::BYTES, vbase, p.sv[2], r0 + kBlk, p.T);
+    }
   };
 
   stage(0, 0);
@@ -664,18 +670,18 @@ __global__ __launch_bounds__(64 * kFwdW8Waves, 2) void attn_fwd_w8_kernel(AttnPa
     if (j < jlast) stage(j + 1, buf ^ 1);
     if (active && j <= jw) {
       if (PEEL || j < jw)
-        fwd32_tile<E, D, false>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
-                                j * kFwdKeys, q0, c2);
+        fwd32_tile<E, D, false, NQ>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                                j * KEYS, q0, c2);
       else
-        fwd32_tile<E, D, true>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
-                               j * kFwdKeys, q0, c2);
+        fwd32_tile<E, D, true, NQ>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+                               j * KEYS, q0, c2);
     }
     wait_vmem();
     __syncthreads();
   }
   if (PEEL && active)  // jw == jlast
-    fwd32_tile<E, D, true>(smem[jlast & 1][0], smem[jlast & 1][1], qop, oacc, mrun, lrun, rbase_op, tbase_op,
-                           lane, jlast * kFwdKeys, q0, c2);
+    fwd32_tile<E, D, true, NQ>(smem[jlast & 1][0], smem[jlast & 1][1], qop, oacc, mrun, lrun, rbase_op, tbase_op,
+                           lane, jlast * KEYS, q0, c2);
 
   if (!active) return;
   const int row = q0 + l32;

@@ -168,6 +168,16 @@ void set_pairs(mt::AttnParams& p, int pairs) {
 #endif
 constexpr int kDq128Waves = MT_DQ128_WAVES;
 
+// Waves per D = 128 forward workgroup: 8 with 128-key K / V tiles (one
+// workgroup per CU, 128 KB of LDS) or 4 with 64-key tiles (two per CU, so a
+// barrier stalls half of a CU's waves).  Measured at BASELINE config 4 (A/B
+// on one box): the forward 0.402 -> 0.383 ms with 4, the fwd+bwd step within
+// 1 % (the kernels after it run at a lower clock).
+#ifndef MT_FWD128_WAVES
+#define MT_FWD128_WAVES 4
+#endif
+constexpr int kFwd128Waves = MT_FWD128_WAVES;
+
 // split = 0: the dK/dV head split of choose_split; else that split (a divisor of R)
 void fill_geometry(mt::AttnParams& p, int B, int Hq, int Hkv, int T, int D, float scale, int split = 0) {
   p.B = B;
@@ -212,9 +222,14 @@ hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
   const int cus = device_cus();
   p.fwd_fold = (MT_FWD_FOLD && (int)grid.x > cus && (int)grid.x <= 2 * cus) ? cus : 0;
   if constexpr (D > 64) {
-    const dim3 block(64 * mt::kFwdW8Waves);
-    return p.rb == 1 ? launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, true>, grid, block, st, p)
-                     : launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, false>, grid, block, st, p);
+    // kFwd128Waves waves per workgroup (kFwd128Waves / 2 (head, row block) pairs)
+    constexpr int keys = kFwd128Waves == 8 ? 128 : 64;
+    mt::AttnParams pf = p;
+    set_pairs(pf, kFwd128Waves / 2);
+    const dim3 grid_w(pf.nsb * pf.B * pf.Hkv * pf.n_hsub), block(64 * kFwd128Waves);
+    return pf.rb == 1
+               ? launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, true, kFwd128Waves, keys>, grid_w, block, st, pf)
+               : launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, false, kFwd128Waves, keys>, grid_w, block, st, pf);
   } else {
     return p.rb == 1 ? launch_main(mt::attn_fwd_kernel<E, D, ROPE, true>, grid, dim3(256), st, p)
                      : launch_main(mt::attn_fwd_kernel<E, D, ROPE, false>, grid, dim3(256), st, p);
