@@ -186,10 +186,6 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t* x, int64
 constexpr float kRescaleSlack = 8.0f;
 constexpr float kSumLimit = 256.0f;  // 2^kRescaleSlack
 constexpr int kFwdKeys = 128;  // keys per staged K/V tile (two 64-row halves)
-#ifndef MT_FWD_VALU_PER_MFMA
-#define MT_FWD_VALU_PER_MFMA 0
-#endif
-constexpr int kFwdValuPerMfma = MT_FWD_VALU_PER_MFMA;  // E(h) VALU slots after each MFMA
 
 // One 128-key tile for one wave (64 query rows, two 32-row column tiles nt).
 // Quarter h = keys kt0 + 32h .. +31.  Pipeline (issue order):
@@ -290,7 +286,6 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
         for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = E::mfma(a, pk[nt][k2], oacc[dt][nt]);
       }
   };
-  constexpr int NP = 4 * DT;       // PV MFMAs of a quarter
 
   f32x16 st[2][2];                 // ring: two quarters' scores [slot][nt]
   V8 pk[2][2][2];                  // ring: two quarters' packed P [slot][nt][k2]
@@ -310,29 +305,8 @@ __device__ __forceinline__ void fwd_tile(const char* K, const char* Vt, const ty
     if (h > 0 && live[h - 1]) pv(h - 1, pk[(h + 1) & 1]);
     if (h < 3 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
     if (live[h]) ex(h, st[h & 1], pk[h & 1], qs);
-    // each MFMA followed by kFwdValuPerMfma VALU instructions of E(h); every
-    // operand read is issued one operand (two MFMAs) ahead
-    if (kFwdValuPerMfma == 0) {
-      // leave the interleaving to the scheduler
-    } else if (h > 0) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, kFwdValuPerMfma, 0);
-      }
-    } else {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    if (kFwdValuPerMfma > 0 && h < 3) {
-#pragma unroll
-      for (int i = 0; i < 2 * KT; ++i) {
-        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, kFwdValuPerMfma, 0);
-      }
-    }
+    // the interleaving inside the stage is left to the scheduler (explicit
+    // sched_group_barrier patterns of k VALU per MFMA measured slower)
     __builtin_amdgcn_sched_barrier(0);
     // C(h): after PV(h-1), so a rescale of O covers everything accumulated
     if (live[h]) chk(h, st[h & 1], pk[h & 1], qs);
