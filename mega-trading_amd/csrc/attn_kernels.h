@@ -459,8 +459,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnParams p) {
 // attn_fwd_kernel (fp32 scale and offset per score, lazy rescaling).
 constexpr int kFwdW8Waves = 8;
 
-// NQ 32-key quarters per staged tile (4: 128 keys, 2: 64 keys).
-template <class E, int D, bool MASK, int NQ = 4>
+// NQ 32-key quarters per staged tile (4: 128 keys, 2: 64 keys).  AHEAD:
+// quarter h+1's scores are issued before quarter h's softmax (two score
+// tiles live); without it one is, for 4 waves per SIMD at D = 64.
+template <class E, int D, bool MASK, int NQ = 4, bool AHEAD = true>
 __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const typename E::v8* qop, f32x16* oacc,
                                            float& mrun, float& lrun, int rbase, TrBase tbase, int lane, int kt0,
                                            int q0, float c2) {
@@ -536,17 +538,21 @@ __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const 
   };
 
   // S(h+1) is issued before E(h) so the score MFMAs overlap the softmax
-  f32x16 st[2];
+  f32x16 st[AHEAD ? 2 : 1];
   V8 pk[2];
-  if (live[0]) sq(0, st[0]);
+  if (AHEAD && live[0]) sq(0, st[0]);
 #pragma unroll
   for (int h = 0; h < NQ; ++h) {
-    if (h < NQ - 1 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
+    if constexpr (AHEAD) {
+      if (h < NQ - 1 && live[h + 1]) sq(h + 1, st[(h + 1) & 1]);
+    } else {
+      if (live[h]) sq(h, st[0]);
+    }
     float qs = 0.f;
-    if (live[h]) qs = ex(h, st[h & 1], pk);
+    if (live[h]) qs = ex(h, st[AHEAD ? (h & 1) : 0], pk);
     __builtin_amdgcn_sched_barrier(0);
     if (live[h]) {
-      chk(h, st[h & 1], pk, qs);
+      chk(h, st[AHEAD ? (h & 1) : 0], pk, qs);
       pv(h, pk);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -555,17 +561,20 @@ __device__ __forceinline__ void fwd32_tile(const char* K, const char* Vt, const 
 
 // NW waves per workgroup (the RowTask's NW / 2 (head, row block) pairs; the
 // launch sets r_sub and rb for that many), KEYS keys per staged K / V tile.
+// Occupancy: two workgroups per CU at D <= 64 (NW / 2 waves per SIMD, so at
+// most 128 VGPRs with NW = 8), two waves per SIMD at D = 128.
 template <class E, int D, bool ROPE, bool PEEL, int NW = kFwdW8Waves, int KEYS = kFwdKeys>
-__global__ __launch_bounds__(64 * NW, 2) void attn_fwd_w8_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * NW, D <= 64 ? NW / 2 : 2) void attn_fwd_w8_kernel(AttnParams p) {
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
   constexpr int NQ = KEYS / 32;
+  constexpr bool kAhead = !(D == 64 && NW == 8);     // register budget of 4 waves per SIMD
   constexpr int SW = TL::INSTR < NW ? TL::INSTR : NW;  // waves that stage tiles
   __shared__ __attribute__((aligned(1024))) char smem[2][2][(KEYS / 64) * TL::BYTES];  // [buf][K, V] x KEYS rows
 
-  const RowTask task = row_task(p, blockIdx.x);
+  const RowTask task = row_task(p, fold_order(blockIdx.x, gridDim.x, p.fwd_fold));
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -644,17 +653,17 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_fwd_w8_kernel(AttnParams p) {
     if (j < jlast) stage(j + 1, buf ^ 1);
     if (active && j <= jw) {
       if (PEEL || j < jw)
-        fwd32_tile<E, D, false, NQ>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+        fwd32_tile<E, D, false, NQ, kAhead>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
                                 j * KEYS, q0, c2);
       else
-        fwd32_tile<E, D, true, NQ>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
+        fwd32_tile<E, D, true, NQ, kAhead>(smem[buf][0], smem[buf][1], qop, oacc, mrun, lrun, rbase_op, tbase_op, lane,
                                j * KEYS, q0, c2);
     }
     wait_vmem();
     __syncthreads();
   }
   if (PEEL && active)  // jw == jlast
-    fwd32_tile<E, D, true, NQ>(smem[jlast & 1][0], smem[jlast & 1][1], qop, oacc, mrun, lrun, rbase_op, tbase_op,
+    fwd32_tile<E, D, true, NQ, kAhead>(smem[jlast & 1][0], smem[jlast & 1][1], qop, oacc, mrun, lrun, rbase_op, tbase_op,
                            lane, jlast * KEYS, q0, c2);
 
   if (!active) return;
@@ -1176,28 +1185,32 @@ constexpr int kKvKpw = 32;     // keys per wave
 constexpr int kKvKeys = kKvWaves * kKvKpw;
 constexpr int kKvRows = 128;   // query rows staged per step (two row blocks)
 
-// One step of a wave: rows [qrow0, qrow0 + 128) of one head against the
-// wave's 32 keys.  Quarter h covers rows qrow0 + 32h.  MFMA / VALU pipeline
+// One step of a wave: rows [qrow0, qrow0 + 32 NQ) of one head against the
+// wave's 32 keys (NQ = 4: both staged 64-row tiles; NQ = 2: the one tile Q,
+// G point at).  Quarter h covers rows qrow0 + 32h.  MFMA / VALU pipeline
 // (issue order, phases fenced by sched_barrier, MFMAs interleaved with the
-// VALU work of the same phase):
+// VALU work of the same phase), for NQ = 4:
 //   SdP0 | SdP1 + V0 | dVdK0 + SdP2 + V1 | dVdK1 + SdP3 + V2 | dVdK2 + V3 | dVdK3
+// and for NQ = 2:  SdP0 | SdP1 + V0 | dVdK0 + V1 | dVdK1
 // where SdPh = S and dP of quarter h, Vh = its softmax / dS, dVdKh = its
-// dV and dK updates.  Quarters with every key above every row are skipped
-// (LIVE masks only matter on the diagonal, where MASK is set).
-template <class E, int D, bool MASK>
+// dV and dK updates.  Quarters with every key above every row, or every row
+// at or past T, are skipped (LIVE masks only matter where MASK is set).
+template <class E, int D, bool MASK, int NQ = 4>
 __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const float* lrow, const float* drow,
                                          const typename E::v8* kop, const typename E::v8* vop,
                                          f32x16* dkacc, f32x16* dvacc, int rbase, TrBase tbase, int lane,
                                          int key, int k0, int qrow0, int T) {
+  static_assert(NQ == 2 || NQ == 4, "one or two 64-row tiles per step");
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
   constexpr int DT = D / 32;
   const int hh = lane >> 5;
-  // quarter live: some key of the wave is <= the quarter's last row
-  bool live[4];
+  // quarter live: some key of the wave is <= the quarter's last row, and the
+  // quarter's first row is below T
+  bool live[NQ];
 #pragma unroll
-  for (int h = 0; h < 4; ++h) live[h] = !MASK || (k0 <= qrow0 + 32 * h + 31);
+  for (int h = 0; h < NQ; ++h) live[h] = !MASK || (k0 <= qrow0 + 32 * h + 31 && qrow0 + 32 * h < T);
 
   auto sdp = [&](int h, f32x16& s, f32x16& dp) {
     const char* Qh = Q + (h >> 1) * TL::BYTES;
@@ -1254,9 +1267,9 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
     MT_DKV_GROUP(0x002, 16);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // phases 3, 4: dVdK(h-2) + SdP(h) + V(h-1), h = 2, 3
+  // phases 3 .. NQ: dVdK(h-2) + SdP(h) + V(h-1), h = 2 .. NQ-1
 #pragma unroll
-  for (int h = 2; h < 4; ++h) {
+  for (int h = 2; h < NQ; ++h) {
     if (live[h - 2]) dvdk(h - 2, pk[h & 1], dk[h & 1]);
     if (live[h]) sdp(h, s[h & 1], dp[h & 1]);
     if (live[h - 1]) vh(h - 1, s[(h - 1) & 1], dp[(h - 1) & 1], pk[(h - 1) & 1], dk[(h - 1) & 1]);
@@ -1274,9 +1287,9 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  // phase 5: dVdK2 + V3
-  if (live[2]) dvdk(2, pk[0], dk[0]);
-  if (live[3]) vh(3, s[1], dp[1], pk[1], dk[1]);
+  // dVdK(NQ-2) + V(NQ-1)
+  if (live[NQ - 2]) dvdk(NQ - 2, pk[0], dk[0]);
+  if (live[NQ - 1]) vh(NQ - 1, s[1], dp[1], pk[1], dk[1]);
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
     MT_DKV_GROUP(0x100, 2);
@@ -1284,8 +1297,8 @@ __device__ __forceinline__ void dkv_step(const char* Q, const char* G, const flo
     MT_DKV_GROUP(0x002, 10);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // phase 6: dVdK3
-  if (live[3]) dvdk(3, pk[1], dk[1]);
+  // dVdK(NQ-1)
+  if (live[NQ - 1]) dvdk(NQ - 1, pk[1], dk[1]);
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
     MT_DKV_GROUP(0x100, 2);
@@ -1302,9 +1315,19 @@ struct DkvLds {
   static constexpr int BYTES = TILES + 2 * 2 * kKvRows * 4;
 };
 
-// One dK/dV workgroup (task L of the dK/dV grid).
-template <class E, int D, bool ROPE>
+// One dK/dV workgroup (task L of the dK/dV grid), KVK keys.
+//  * KVK = 128: wave w owns keys 32w .. 32w+31 of the block and runs every
+//    staged 128-row step on them.
+//  * KVK = 64: waves w and w+2 own keys 32(w & 1) .. +31; of each staged
+//    128-row step wave w takes the first 64 rows and wave w+2 the second,
+//    and the pair adds its dK / dV through LDS at the end.  A task then
+//    carries half the work, so the heaviest (first) key blocks, which bound
+//    the launch when the grid is one or two resident rounds, finish twice as
+//    soon.
+template <class E, int D, bool ROPE, int KVK = kKvKeys>
 __device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) {
+  static_assert(KVK == 128 || KVK == 64, "128 or 64 keys per task");
+  constexpr int NQ = KVK == 128 ? 4 : 2;      // 32-row quarters per wave and step
   using V8 = typename E::v8;
   using TL = Tile<D>;
   constexpr int KT = D / 16;
@@ -1326,8 +1349,10 @@ __device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) 
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int hh = lane >> 5;
-  const int k0 = kb * kKvKeys + wave * kKvKpw;   // this wave's first key
-  const int key = k0 + l32;                      // this lane's key (C column)
+  const int kcol = KVK == 128 ? wave : (wave & 1);  // key column of the wave
+  const int rsel = KVK == 128 ? 0 : (wave >> 1);    // its 64-row half of a step (KVK = 64)
+  const int k0 = kb * KVK + kcol * kKvKpw;         // this wave's first key
+  const int key = k0 + l32;                        // this lane's key (C column)
   const bool wave_live = k0 < p.T;
 
   // K and V rows as B operands (N = key, k = d).  K is pre-multiplied by
@@ -1361,7 +1386,7 @@ __device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) 
   // (uneven when n_split does not divide R)
   const int h_lo = (p.R * hs) / p.n_split;
   const int hpt = (p.R * (hs + 1)) / p.n_split - h_lo;  // heads per task
-  const int qr0 = kb * kKvKeys;                    // first row touching these keys (128-aligned)
+  const int qr0 = kb * KVK;                        // first row touching these keys
   const int nstep_h = (p.T - qr0 + kKvRows - 1) / kKvRows;  // 128-row steps per head
   const int n_it = hpt * nstep_h;
 
@@ -1400,19 +1425,59 @@ __device__ __forceinline__ void dkv_body(const AttnParams& p, int L, char* lds) 
     }
     if (it + 1 < n_it) stage(nxt_head, nxt_row, buf ^ 1);
     if (wave_live) {
+      // this wave's rows of the step: all 128, or its 64-row half
+      const int row0 = cur_row + 64 * rsel;
+      const char* Qw = smem[buf][0] + rsel * TL::BYTES;
+      const char* Gw = smem[buf][1] + rsel * TL::BYTES;
+      const float* lw = vec[buf][0] + 64 * rsel;
+      const float* dw = vec[buf][1] + 64 * rsel;
       // no mask when every key of the wave precedes every row and all rows are below T
-      const bool fast = (k0 + kKvKpw - 1 <= cur_row) && (cur_row + kKvRows <= p.T);
+      const bool fast = (k0 + kKvKpw - 1 <= row0) && (row0 + 32 * NQ <= p.T);
       if (fast)
-        dkv_step<E, D, false>(smem[buf][0], smem[buf][1], vec[buf][0], vec[buf][1], kop, vop, dkacc, dvacc,
-                              rbase_op, tbase_op, lane, key, k0, cur_row, p.T);
+        dkv_step<E, D, false, NQ>(Qw, Gw, lw, dw, kop, vop, dkacc, dvacc, rbase_op, tbase_op, lane, key, k0, row0,
+                                  p.T);
       else
-        dkv_step<E, D, true>(smem[buf][0], smem[buf][1], vec[buf][0], vec[buf][1], kop, vop, dkacc, dvacc,
-                             rbase_op, tbase_op, lane, key, k0, cur_row, p.T);
+        dkv_step<E, D, true, NQ>(Qw, Gw, lw, dw, kop, vop, dkacc, dvacc, rbase_op, tbase_op, lane, key, k0, row0,
+                                 p.T);
     }
     wait_vmem();
     __syncthreads();
   }
 
+  if constexpr (KVK == 64) {
+    // waves 2, 3 hand their sums to waves 0, 1 (same keys) through the
+    // staging LDS, free after the loop's last barrier: [kcol][slot][lane]
+    // 16-byte chunks, conflict-free
+    constexpr int NV = DT * 16 / 4;   // f32x4 chunks per accumulator set
+    f32x4* red = reinterpret_cast<f32x4*>(lds);
+    if (rsel == 1 && wave_live) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          red[((kcol * 2 * NV) + dt * 4 + g4) * 64 + lane] =
+              f32x4{dkacc[dt][4 * g4], dkacc[dt][4 * g4 + 1], dkacc[dt][4 * g4 + 2], dkacc[dt][4 * g4 + 3]};
+          red[((kcol * 2 * NV) + NV + dt * 4 + g4) * 64 + lane] =
+              f32x4{dvacc[dt][4 * g4], dvacc[dt][4 * g4 + 1], dvacc[dt][4 * g4 + 2], dvacc[dt][4 * g4 + 3]};
+        }
+    }
+    __syncthreads();
+    if (rsel == 1) return;
+    if (wave_live) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 a = red[((kcol * 2 * NV) + dt * 4 + g4) * 64 + lane];
+          const f32x4 b = red[((kcol * 2 * NV) + NV + dt * 4 + g4) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dkacc[dt][4 * g4 + e] += a[e];
+            dvacc[dt][4 * g4 + e] += b[e];
+          }
+        }
+    }
+  }
   if (!wave_live || key >= p.T) return;
   if (p.n_split == 1) {
     uint16_t* dkrow = p.dk + b * p.sdk[0] + (int64_t)kvh * p.sdk[1] + (int64_t)key * p.sdk[2];
@@ -1473,26 +1538,36 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
 // keeps that: it interleaves chunks of 8 consecutive workgroups, each chunk
 // one kind, so task index and workgroup index agree mod 8 and the dQ and
 // dK/dV tasks of a group share one XCD's L2 (its K/V and Q/dO rows).  When a
-// count is not a multiple of 8 the merge is per workgroup.
+// count is not a multiple of 8 the merge is per workgroup.  KVK = keys per
+// dK/dV task (dkv_body).
 template <int D>
 struct BwdLds {
   static constexpr int BYTES = DqLds<D>::BYTES > DkvLds<D>::BYTES ? DqLds<D>::BYTES : DkvLds<D>::BYTES;
 };
 
-template <class E, int D, bool ROPE, bool PEEL>
+template <class E, int D, bool ROPE, bool PEEL, int KVK>
 __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnParams p) {
   static_assert(kKvWaves == 4, "dQ and dK/dV workgroups must have the same size");
   __shared__ __attribute__((aligned(1024))) char lds[BwdLds<D>::BYTES];
   const int L = blockIdx.x;
   const int sh = ((p.n_kv_tasks | p.n_dq_tasks) & 7) == 0 ? 3 : 0;  // chunks of 8 workgroups, or of 1
-  const int c = L >> sh;
   const int n = (p.n_kv_tasks + p.n_dq_tasks) >> sh;
+  // Within an XCD, consecutive workgroups go to its 4 shader engines in turn
+  // and are dispatched in order, so an engine with no free slot holds back
+  // the next workgroups of every engine.  With a 1:1 interleave, chunk c's
+  // kind would repeat with c mod 4 and each engine would get one kind only;
+  // rotating the chunks of each block of 4 (32 single workgroups) by the
+  // block index gives every engine both kinds in the interleave's
+  // proportion.  A permutation of complete blocks: every task runs once.
+  const int P = sh ? 4 : 32;
+  const int u = L >> sh, m = u / P, t = u - m * P;
+  const int c = (m + 1) * P <= n ? m * P + (t + m) % P : u;
   const int nkv = p.n_kv_tasks >> sh;
   const int kv_before = (int)((int64_t)c * nkv / n);
   const int kv_through = (int)((int64_t)(c + 1) * nkv / n);
-  const int sub = L - (c << sh);
+  const int sub = L - (u << sh);
   if (kv_through > kv_before)
-    dkv_body<E, D, ROPE>(p, (kv_before << sh) + sub, lds);
+    dkv_body<E, D, ROPE, KVK>(p, (kv_before << sh) + sub, lds);
   else
     dq_body<E, D, ROPE, PEEL>(p, ((c - kv_before) << sh) + sub, lds);
 }

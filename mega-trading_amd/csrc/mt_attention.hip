@@ -199,6 +199,12 @@ void copy3(int64_t dst[3], const int64_t* s) {
   dst[2] = s[2];
 }
 
+// D <= 64 forward with 8 waves of 32 rows (attn_fwd_w8_kernel) instead of 4 of
+// 64: 0 never, 1 when the grid is one resident round, 2 always
+#ifndef MT_FWD64_W8
+#define MT_FWD64_W8 1
+#endif
+
 template <class E, int D, bool ROPE>
 hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
   if (ROPE) {
@@ -213,34 +219,68 @@ hipError_t launch_fwd(mt::AttnParams p, hipStream_t st, int) {
     p.sk[1] = (int64_t)p.T * D;
     p.sk[2] = D;
   }
-  dim3 grid(p.nsb * p.B * p.Hkv * p.n_hsub);
 #ifndef MT_FWD_FOLD
 #define MT_FWD_FOLD 1
 #endif
   // one resident round (more than one and at most two workgroups per CU):
   // pair heavy and light row blocks on each CU
   const int cus = device_cus();
-  p.fwd_fold = (MT_FWD_FOLD && (int)grid.x > cus && (int)grid.x <= 2 * cus) ? cus : 0;
+  auto fold = [&](int grid) { return (MT_FWD_FOLD && grid > cus && grid <= 2 * cus) ? cus : 0; };
+  const dim3 grid(p.nsb * p.B * p.Hkv * p.n_hsub);
+  p.fwd_fold = fold((int)grid.x);
   if constexpr (D > 64) {
     // kFwd128Waves waves per workgroup (kFwd128Waves / 2 (head, row block) pairs)
     constexpr int keys = kFwd128Waves == 8 ? 128 : 64;
     mt::AttnParams pf = p;
     set_pairs(pf, kFwd128Waves / 2);
     const dim3 grid_w(pf.nsb * pf.B * pf.Hkv * pf.n_hsub), block(64 * kFwd128Waves);
+    pf.fwd_fold = fold((int)grid_w.x);
     return pf.rb == 1
                ? launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, true, kFwd128Waves, keys>, grid_w, block, st, pf)
                : launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, false, kFwd128Waves, keys>, grid_w, block, st, pf);
   } else {
+    if (MT_FWD64_W8 == 2 || (MT_FWD64_W8 == 1 && (int)grid.x <= 2 * cus)) {
+      // one resident round: 8 waves of 32 rows, so the longest row blocks
+      // run as two waves per SIMD rather than one
+      const dim3 block(512);
+      return p.rb == 1 ? launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, true, 8, 128>, grid, block, st, p)
+                       : launch_main(mt::attn_fwd_w8_kernel<E, D, ROPE, false, 8, 128>, grid, block, st, p);
+    }
     return p.rb == 1 ? launch_main(mt::attn_fwd_kernel<E, D, ROPE, true>, grid, dim3(256), st, p)
                      : launch_main(mt::attn_fwd_kernel<E, D, ROPE, false>, grid, dim3(256), st, p);
   }
+}
+
+// Keys per dK/dV task in the one-launch backward (D <= 64): 128, or 64 when
+// the launch is bound by its longest tasks rather than by throughput.  The
+// task of key block 0 covers every row of its heads; when that work exceeds
+// 1.5x the average a workgroup slot (two per CU) has to do, the
+// heaviest-first order cannot hide it and the launch ends with those tasks
+// running nearly alone (short sequences with few KV groups: BASELINE config
+// 2 has 2.1x, config 3 1.1x, the config 5 layer 1.0x).  Work is counted in
+// MFMAs per wave: 48 per (64-row block, 64 keys) of a dQ wave, 64 per (32
+// keys, 128 rows) of a dK/dV wave.
+#ifndef MT_DKV_KEYS
+#define MT_DKV_KEYS 0  // 0: by the rule above; 64 or 128: always that
+#endif
+int merged_dkv_keys(const mt::AttnParams& p) {
+  if (MT_DKV_KEYS == 64 || MT_DKV_KEYS == 128) return MT_DKV_KEYS;
+  const double steps = (p.T + 127) / 128;                  // 128-row steps of key block 0
+  const double hpt = (p.R + p.n_split - 1) / p.n_split;    // heads of the largest task
+  const double heavy = 64.0 * hpt * steps;
+  const double nqb = p.nqb;
+  const double dq = 48.0 * p.B * p.Hq * nqb * (nqb + 1) / 2 / 4;
+  const double kv = 64.0 * p.B * p.Hq * steps * (steps + 1) / 2;
+  const double mean = (dq + kv) / (2.0 * device_cus());
+  return heavy > 1.5 * mean ? 64 : 128;
 }
 
 // stage: 1 = prep (delta, LSE log2 e) + dQ, 2 = dK/dV (reads the prep vectors), 3 = all
 template <class E, int D, bool ROPE>
 hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
   const int n_dq = p.nsb * p.B * p.Hkv * p.n_hsub;
-  const int n_kv = p.nkb * p.B * p.Hkv * p.n_split;
+  const int kvk = D <= 64 ? merged_dkv_keys(p) : mt::kKvKeys;
+  const int n_kv = (p.T + kvk - 1) / kvk * p.B * p.Hkv * p.n_split;
   if (D <= 64 && (stage & 1)) {
     // -delta and -LSE log2(e) for both kinds of task (at D = 128 the dQ
     // kernel, which runs first, writes them)
@@ -256,8 +296,13 @@ hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
     p.n_dq_tasks = (stage & 1) ? n_dq : 0;
     p.n_kv_tasks = (stage & 2) ? n_kv : 0;
     const dim3 grid(p.n_dq_tasks + p.n_kv_tasks);
-    hipError_t e = p.rb == 1 ? launch_main(mt::attn_bwd_kernel<E, D, ROPE, true>, grid, dim3(256), st, p)
-                             : launch_main(mt::attn_bwd_kernel<E, D, ROPE, false>, grid, dim3(256), st, p);
+    hipError_t e;
+    if (kvk == 64)
+      e = p.rb == 1 ? launch_main(mt::attn_bwd_kernel<E, D, ROPE, true, 64>, grid, dim3(256), st, p)
+                    : launch_main(mt::attn_bwd_kernel<E, D, ROPE, false, 64>, grid, dim3(256), st, p);
+    else
+      e = p.rb == 1 ? launch_main(mt::attn_bwd_kernel<E, D, ROPE, true, 128>, grid, dim3(256), st, p)
+                    : launch_main(mt::attn_bwd_kernel<E, D, ROPE, false, 128>, grid, dim3(256), st, p);
     if (e != hipSuccess) return e;
   } else {
     if (stage & 1) {
