@@ -73,6 +73,10 @@ struct AttnParams {
   int n_kv_tasks; // attn_bwd_kernel: dK/dV workgroups in the grid
   int n_dq_tasks; // attn_bwd_kernel: dQ workgroups in the grid
   int fwd_fold;   // forward grids of one resident round: workgroups past this index run in reverse order (0: off)
+  // attn_bwd_kernel task order, in chunks (of 8 workgroups, or of 1): mg_head
+  // chunks of one kind (dK/dV if mg_head_kv), then mg_mid_kv dK/dV and
+  // mg_mid_dq dQ chunks interleaved in proportion, then the rest of one kind
+  int mg_head, mg_head_kv, mg_mid_kv, mg_mid_dq;
   float scale;       // softmax scale (1/sqrt(D) by default)
   float scale_log2;  // scale * log2(e)
 };
@@ -1526,20 +1530,22 @@ __global__ __launch_bounds__(64 * kKvWaves, D <= 64 ? 2 : 1) void attn_bwd_dkv_k
 // Backward, dQ and dK/dV work in one launch (D <= 64)
 // ===========================================================================
 // The n_kv dK/dV tasks and the n_dq dQ tasks are independent once the prep
-// pass has written -delta and -LSE log2(e), so one grid holds both, merged by
-// a proportional interleave (a dK/dV task where floor(i n_kv / N) steps).
-// Both task lists are heaviest first, so the merged order is close to
-// heaviest first overall and the light tasks of either kind fill the slots
-// the other kind's long tasks leave at the end.
+// pass has written -delta and -LSE log2(e), so one grid holds both, in
+// longest-first order over both kinds: both lists are sorted by work, and the
+// host (bwd_merge) describes their merge as a head of the kind whose tasks are
+// longer than every task of the other, a middle where the two interleave in
+// proportion, and a tail of the kind whose tasks are shorter than every task
+// of the other.  The last workgroups to start are then the shortest of either
+// kind, which keeps the end of the launch short.
 //
 // Workgroups are dealt to the 8 XCDs round-robin by index, and both task
 // lists give task i the (batch, KV head) group i mod (B Hkv) (times the
 // head split), so with 8 | B Hkv a task's group decides its XCD.  The merge
-// keeps that: it interleaves chunks of 8 consecutive workgroups, each chunk
-// one kind, so task index and workgroup index agree mod 8 and the dQ and
-// dK/dV tasks of a group share one XCD's L2 (its K/V and Q/dO rows).  When a
-// count is not a multiple of 8 the merge is per workgroup.  KVK = keys per
-// dK/dV task (dkv_body).
+// keeps that: it orders chunks of 8 consecutive workgroups, each chunk one
+// kind, so task index and workgroup index agree mod 8 and the dQ and dK/dV
+// tasks of a group share one XCD's L2 (its K/V and Q/dO rows).  When a count
+// is not a multiple of 8 the merge is per workgroup.  KVK = keys per dK/dV
+// task (dkv_body).
 template <int D>
 struct BwdLds {
   static constexpr int BYTES = DqLds<D>::BYTES > DkvLds<D>::BYTES ? DqLds<D>::BYTES : DkvLds<D>::BYTES;
@@ -1554,22 +1560,38 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnParams p) {
   const int n = (p.n_kv_tasks + p.n_dq_tasks) >> sh;
   // Within an XCD, consecutive workgroups go to its 4 shader engines in turn
   // and are dispatched in order, so an engine with no free slot holds back
-  // the next workgroups of every engine.  With a 1:1 interleave, chunk c's
-  // kind would repeat with c mod 4 and each engine would get one kind only;
-  // rotating the chunks of each block of 4 (32 single workgroups) by the
-  // block index gives every engine both kinds in the interleave's
-  // proportion.  A permutation of complete blocks: every task runs once.
+  // the next workgroups of every engine.  Where the two kinds interleave 1:1,
+  // chunk c's kind would repeat with c mod 4 and each engine would get one
+  // kind only; rotating the chunks of each block of 4 (32 single workgroups)
+  // by the block index gives every engine both kinds.  A permutation of
+  // complete blocks: every task runs once.
   const int P = sh ? 4 : 32;
   const int u = L >> sh, m = u / P, t = u - m * P;
   const int c = (m + 1) * P <= n ? m * P + (t + m) % P : u;
-  const int nkv = p.n_kv_tasks >> sh;
-  const int kv_before = (int)((int64_t)c * nkv / n);
-  const int kv_through = (int)((int64_t)(c + 1) * nkv / n);
   const int sub = L - (u << sh);
-  if (kv_through > kv_before)
-    dkv_body<E, D, ROPE, KVK>(p, (kv_before << sh) + sub, lds);
+  const int nkv = p.n_kv_tasks >> sh;
+  const int kv0 = p.mg_head_kv ? p.mg_head : 0;    // first dK/dV chunk of the middle
+  const int dq0 = p.mg_head_kv ? 0 : p.mg_head;    // first dQ chunk of the middle
+  const int mid = p.mg_mid_kv + p.mg_mid_dq;
+  bool kv;
+  int idx;
+  if (c < p.mg_head) {
+    kv = p.mg_head_kv;
+    idx = c;
+  } else if (c < p.mg_head + mid) {
+    const int j = c - p.mg_head;
+    const int before = (int)((int64_t)j * p.mg_mid_kv / mid);
+    kv = (int)((int64_t)(j + 1) * p.mg_mid_kv / mid) > before;
+    idx = kv ? kv0 + before : dq0 + (j - before);
+  } else {
+    const int j = c - p.mg_head - mid;
+    kv = kv0 + p.mg_mid_kv < nkv;
+    idx = kv ? kv0 + p.mg_mid_kv + j : dq0 + p.mg_mid_dq + j;
+  }
+  if (kv)
+    dkv_body<E, D, ROPE, KVK>(p, (idx << sh) + sub, lds);
   else
-    dq_body<E, D, ROPE, PEEL>(p, ((c - kv_before) << sh) + sub, lds);
+    dq_body<E, D, ROPE, PEEL>(p, (idx << sh) + sub, lds);
 }
 
 // ===========================================================================

@@ -7,6 +7,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -275,6 +276,46 @@ int merged_dkv_keys(const mt::AttnParams& p) {
   return heavy > 1.5 * mean ? 64 : 128;
 }
 
+// Longest-first order of the one-launch backward (attn_bwd_kernel): both task
+// lists are already sorted by work (MFMAs per wave, as in merged_dkv_keys);
+// their merge is described as a head of the kind longer than every task of
+// the other, a proportional middle, and a tail of the kind shorter than every
+// task of the other.  Measured at BASELINE config 3 against a proportional
+// interleave of the whole lists (which starts the medium dK/dV tasks last):
+// see the design notes; the end of the launch is its shortest tasks.
+void bwd_merge(mt::AttnParams& p, int kvk) {
+  const int sh = ((p.n_kv_tasks | p.n_dq_tasks) & 7) == 0 ? 3 : 0;
+  const int nk = p.n_kv_tasks >> sh, nd = p.n_dq_tasks >> sh;
+  p.mg_mid_kv = p.mg_mid_dq = 0;
+  if (nk == 0 || nd == 0) {
+    p.mg_head = nk + nd;
+    p.mg_head_kv = nk > 0;
+    return;
+  }
+  const long hpt = (p.R + p.n_split - 1) / p.n_split;
+  const int kv_groups = p.B * p.Hkv * p.n_split, dq_groups = p.B * p.Hkv * p.n_hsub;
+  auto wk = [&](int q) {
+    const int kb = (q << sh) / kv_groups;
+    return (kvk == 128 ? 64L : 32L) * hpt * ((p.T - kvk * kb + 127) / 128);
+  };
+  auto wd = [&](int r) {
+    const int sb = p.nsb - 1 - (r << sh) / dq_groups;
+    return 48L * std::min((sb + 1) * p.rb, p.nqb);
+  };
+  auto count_k = [&](auto pred) { int c = 0; for (int q = 0; q < nk; ++q) c += pred(wk(q)); return c; };
+  auto count_d = [&](auto pred) { int c = 0; for (int r = 0; r < nd; ++r) c += pred(wd(r)); return c; };
+  const long k_max = wk(0), k_min = wk(nk - 1), d_max = wd(0), d_min = wd(nd - 1);
+  int head_k = 0, head_d = 0, tail_k = 0, tail_d = 0;
+  if (k_max > d_max) head_k = count_k([&](long w) { return w > d_max; });
+  else if (d_max > k_max) head_d = count_d([&](long w) { return w > k_max; });
+  if (k_min > d_min) tail_d = count_d([&](long w) { return w < k_min; });
+  else if (d_min > k_min) tail_k = count_k([&](long w) { return w < d_min; });
+  p.mg_head_kv = head_k > 0 || head_d == 0;
+  p.mg_head = head_k + head_d;
+  p.mg_mid_kv = std::max(0, nk - head_k - tail_k);
+  p.mg_mid_dq = std::max(0, nd - head_d - tail_d);
+}
+
 // stage: 1 = prep (delta, LSE log2 e) + dQ, 2 = dK/dV (reads the prep vectors), 3 = all
 template <class E, int D, bool ROPE>
 hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
@@ -295,6 +336,7 @@ hipError_t launch_bwd(mt::AttnParams p, hipStream_t st, int stage) {
     // dQ and dK/dV tasks in one grid
     p.n_dq_tasks = (stage & 1) ? n_dq : 0;
     p.n_kv_tasks = (stage & 2) ? n_kv : 0;
+    bwd_merge(p, kvk);
     const dim3 grid(p.n_dq_tasks + p.n_kv_tasks);
     hipError_t e;
     if (kvk == 64)
