@@ -103,8 +103,21 @@ def rope_tables(t, d, theta, device):
     return freqs.cos().to(device), freqs.sin().to(device)
 
 
-def time_op_steps(pkg, cfg, steps, warmup, rope=True):
-    """Wall time of `steps` fwd+bwd steps through the public op (events + sync)."""
+REPEATS = 5           # timed windows per measurement; the median is reported
+MIN_WARMUP = 25       # warm-up steps before the timed windows (the reference harness: 25)
+PREHEAT_S = 0.5       # and at least this long of back-to-back steps
+
+
+def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s=PREHEAT_S):
+    """fwd+bwd steps through the public op, timed in steady state.
+
+    `warmup` untimed steps, then one timed window of `steps` steps (the cold
+    window: the clock right after warm-up), then more untimed steps until at
+    least MIN_WARMUP steps and `preheat_s` seconds of back-to-back steps have
+    run, then `repeats` timed windows of exactly `steps` steps each, every
+    window bracketed by synchronisation and HIP events on the current stream.
+    Returns ms per step: median, fastest and slowest window, the cold
+    window, and the median window's wall-clock time per step."""
     b, t, hq, hkv, d = cfg
     dev = torch.device("cuda:0")
     q, k, v, do = make_inputs(cfg, dev)
@@ -120,18 +133,30 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True):
             out = pkg.attention(q, k, v, repeats=hq // hkv)
         return torch.autograd.grad(out, (q, k, v), do)
 
+    def window():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps, (time.perf_counter() - t0) / steps * 1e3
+
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / steps, wall / steps * 1e3
+    cold, _ = window()
+    t0, n = time.perf_counter(), warmup + steps
+    while n < MIN_WARMUP or time.perf_counter() - t0 < preheat_s:
+        for _ in range(8):
+            step()
+        n += 8
+        torch.cuda.synchronize()
+    runs = sorted(window() for _ in range(repeats))
+    med_ms, med_wall = runs[len(runs) // 2]
+    return {"ms": med_ms, "ms_min": runs[0][0], "ms_max": runs[-1][0], "ms_cold": cold, "wall_ms": med_wall,
+            "repeats": repeats, "warmup_steps": n}
 
 
 # The reference's own configs use other query-heads-per-KV-head ratios R:
@@ -144,11 +169,12 @@ GROUP_SIZE_CASES = {"R1": (4, 4096, 16, 16, 64), "R2": (4, 4096, 16, 8, 64), "R3
 
 def time_group_sizes(pkg, steps):
     """fwd+bwd TFLOP/s of the fused-RoPE op at each group size R (same FLOP
-    convention; the FLOPs scale with Hq) and each one's ratio to R = 4."""
+    convention; the FLOPs scale with Hq) and each one's ratio to R = 4, timed
+    as the headline is (median of REPEATS windows after the preheat)."""
     out = {}
     for name, cfg in GROUP_SIZE_CASES.items():
         b, t, hq, hkv, d = cfg
-        ms, _ = time_op_steps(pkg, cfg, steps, 3, rope=True)
+        ms = time_op_steps(pkg, cfg, steps, 3, rope=True)["ms"]
         out[name] = {"Hq": hq, "Hkv": hkv, "ms": round(ms, 4), "tflops": round(fwd_bwd_flops(b, t, hq, d) / (ms * 1e-3) / 1e12, 1)}
     for name in out:
         out[name]["vs_R4"] = round(out[name]["tflops"] / out["R4"]["tflops"], 3)
@@ -354,25 +380,31 @@ def hbm_traffic(kernel):
     return None
 
 
-def cpu_model_name() -> str:
-    """The host CPU's "Model name" line as lscpu prints it (/proc/cpuinfo's
-    "model name" when lscpu is unavailable)."""
+def lscpu_fields() -> dict:
+    """lscpu's "key: value" lines (first occurrence of each key); {} when lscpu is unavailable."""
     import subprocess
 
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        fields = {}
-        for line in out.splitlines():
-            if ":" in line:
-                key, val = line.split(":", 1)
-                fields.setdefault(key.strip(), val.strip())
-        if "Model name" in fields:
-            # a virtualised host may report only the product family: add lscpu's
-            # family / model / stepping numbers, which identify the part
-            ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if k in fields]
-            return fields["Model name"] + (f" ({', '.join(ids)})" if ids else "")
     except (OSError, subprocess.SubprocessError):
-        pass
+        return fields
+    for line in out.splitlines():
+        if ":" in line:
+            key, val = line.split(":", 1)
+            fields.setdefault(key.strip(), val.strip())
+    return fields
+
+
+def cpu_model_name(fields=None) -> str:
+    """The host CPU's "Model name" line as lscpu prints it (/proc/cpuinfo's
+    "model name" when lscpu is unavailable)."""
+    fields = lscpu_fields() if fields is None else fields
+    if "Model name" in fields:
+        # a virtualised host may report only the product family: add lscpu's
+        # family / model / stepping numbers, which identify the part
+        ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if k in fields]
+        return fields["Model name"] + (f" ({', '.join(ids)})" if ids else "")
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -382,13 +414,44 @@ def cpu_model_name() -> str:
     return ""
 
 
+def cpu_quota() -> int | None:
+    """CPUs this process's cgroup may use (cgroup v2 cpu.max), None when unlimited or unknown."""
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            return max(1, int(int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def cpu_threads(fields):
+    """Threads for the CPU baseline: the host's physical cores (lscpu sockets x
+    cores per socket), capped by the CPUs this process may run on (its
+    affinity mask and cgroup quota).  Returns (threads, description)."""
+    try:
+        physical = int(fields["Socket(s)"]) * int(fields["Core(s) per socket"])
+    except (KeyError, ValueError):
+        physical = os.cpu_count() or 1
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = cpu_quota()
+    threads = max(1, min(physical, allowed, quota or allowed))
+    topo = ", ".join(f"{k}: {fields[k]}" for k in ("Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)")
+                     if k in fields)
+    desc = (f"lscpu {topo}; physical cores {physical}; CPUs this process may use: affinity {allowed}, "
+            f"cgroup quota {quota if quota else 'none'}; threads used {threads}")
+    return threads, desc
+
+
 def cpu_baseline(cfg):
     """Reference CPU attention (torch SDPA fp32 fwd + autograd bwd) on one batch
-    element of the workload, 1 warm-up + 3 timed repeats, median."""
+    element of the workload, 1 warm-up + 3 timed repeats, median, on the
+    host's physical cores (those this process may use)."""
     from oracle.sdpa_cpu import sdpa_forward_backward
 
     b, t, hq, hkv, d = cfg
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    fields = lscpu_fields()
+    threads, topo = cpu_threads(fields)
     torch.set_num_threads(threads)
     sample = (1, t, hq, hkv, d)
     q, k, v, do = (x.float() for x in make_inputs(sample, "cpu"))
@@ -400,7 +463,7 @@ def cpu_baseline(cfg):
             times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    model = cpu_model_name()
+    model = cpu_model_name(fields)
     return {
         "value": fwd_bwd_flops(1, t, hq, d) / med / 1e12,
         "unit": "TFLOP/s",
@@ -408,7 +471,7 @@ def cpu_baseline(cfg):
         "kind": "reference",
         "sample": f"torch SDPA fp32 fwd+bwd (reference eager path, model.py:228-235) on 1 of {b} batch elements "
                   f"of the workload (B=1,T={t},Hq={hq},Hkv={hkv},D={d}), median of 3 after 1 warm-up: "
-                  f"{med * 1e3:.1f} ms; host '{model}', os.cpu_count()={os.cpu_count()}",
+                  f"{med * 1e3:.1f} ms; host '{model}', {topo}, os.cpu_count()={os.cpu_count()}",
     }
 
 
@@ -616,8 +679,8 @@ def generate_tokens_per_second(pkg, rollouts=32, prompt=512, new_tokens=64):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-train", action="store_true", help="skip the config 5 train-step tokens/sec leg")
     ap.add_argument("--ops-only", action="store_true",
@@ -649,18 +712,20 @@ def main(argv=None) -> int:
         return 0
 
     b, t, hq, hkv, d = C3
-    ms_event, ms_wall = time_op_steps(pkg, C3, args.steps, args.warmup, rope=True)
+    head = time_op_steps(pkg, C3, args.steps, args.warmup, rope=True)
+    ms_event = head["ms"]
     flops = fwd_bwd_flops(b, t, hq, d)
     value = flops / (ms_event * 1e-3) / 1e12
+    tflops = lambda ms: round(flops / (ms * 1e-3) / 1e12, 2)  # noqa: E731
 
     kern = time_kernels(pkg, C3, max(10, args.steps // 2))
     dom = max((n for n in kern if "[" not in n), key=lambda n: kern[n]["ms"])
     achieved = kern[dom]["tflops"]
 
-    ms_c2, _ = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)
-    group_sizes = time_group_sizes(pkg, max(10, args.steps // 3))
-    ms_c3_plain, _ = time_op_steps(pkg, C3, max(10, args.steps // 2), 3, rope=False)
-    ms_c4, _ = time_op_steps(pkg, C4, max(10, args.steps // 4), 3, rope=True)
+    ms_c2 = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)["ms"]
+    group_sizes = time_group_sizes(pkg, args.steps)
+    ms_c3_plain = time_op_steps(pkg, C3, args.steps, 3, rope=False)["ms"]
+    ms_c4 = time_op_steps(pkg, C4, max(10, args.steps // 2), 3, rope=True)["ms"]
     ceiling = mfma_ceiling()
     ops_line = time_ops(pkg)
 
@@ -672,6 +737,14 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_event, 4),
+        "timing": {
+            "method": f"median of {head['repeats']} windows of {args.steps} steps (HIP events, current stream), "
+                      f"after {args.warmup} warm-up steps, one cold window and a preheat to at least "
+                      f"{MIN_WARMUP} steps and {PREHEAT_S} s of back-to-back steps ({head['warmup_steps']} run)",
+            "ms_median": round(head["ms"], 4), "ms_fastest": round(head["ms_min"], 4),
+            "ms_slowest": round(head["ms_max"], 4), "tflops_slowest": tflops(head["ms_max"]),
+            "ms_cold_window": round(head["ms_cold"], 4), "tflops_cold_window": tflops(head["ms_cold"]),
+        },
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -702,7 +775,7 @@ def main(argv=None) -> int:
             "C3_unfused_rope_free_tflops": round(flops / (ms_c3_plain * 1e-3) / 1e12, 2),
             "C4_fwd_bwd_tflops": round(fwd_bwd_flops(C4[0], C4[1], C4[2], C4[4]) / (ms_c4 * 1e-3) / 1e12, 2),
             "C4_ms_per_step": round(ms_c4, 4),
-            "wall_ms_per_step": round(ms_wall, 4),
+            "wall_ms_per_step": round(head["wall_ms"], 4),
             "group_sizes": group_sizes,
         },
     }

@@ -66,6 +66,7 @@ extern "C" {
 #define MT_E_DTYPE (-4)     /* dtype code not supported */
 #define MT_E_ROPE (-5)      /* exactly one of rope_cos / rope_sin given */
 #define MT_E_WORKSPACE (-6) /* backward workspace smaller than required */
+#define MT_E_DEVICE (-7)    /* the stream belongs to a device other than the current one */
 
 /* Library version, (major << 16) | minor. */
 int mt_version(void);
@@ -88,8 +89,15 @@ int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float*
                     const float* rope_cos, const float* rope_sin, void* stream);
 
 /* Bytes of device workspace mt_gqa_attn_bwd needs for this shape on the
- * current device (0 for an invalid shape). */
+ * current device (0 for an invalid shape), for 16-bit inputs: an upper bound
+ * for every dtype (fp32 inputs need only the delta / LSE vectors). */
 size_t mt_gqa_attn_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D);
+
+/* As mt_gqa_attn_bwd_workspace_size for one dtype (MT_DTYPE_*): the exact
+ * size mt_gqa_attn_bwd checks against for that dtype.  No separate reference
+ * counterpart: the reference's backward allocates its own buffers
+ * (triton_attention.py:88-111, 148-150). */
+size_t mt_gqa_attn_bwd_workspace_size_dtype(int B, int Hq, int Hkv, int T, int D, int dtype);
 
 /*
  * Backward.  Given dO, writes dQ, dK, dV.
@@ -97,7 +105,7 @@ size_t mt_gqa_attn_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D);
  *   k_rot when RoPE tables are given, in which case dQ and dK are rotated back
  *   by -theta and returned in the un-rotated basis (triton_ops.py:205-214).
  *   workspace: 256-byte aligned device buffer of at least
- *   mt_gqa_attn_bwd_workspace_size() bytes (delta = rowsum(O * dO),
+ *   mt_gqa_attn_bwd_workspace_size_dtype() bytes (delta = rowsum(O * dO),
  *   triton_attention.py:561, and fp32 dK/dV partial sums).
  *   strides: 32 int64 = q, k, v, o, dO, dQ, dK, dV, 4 each in (b, h, t, d) order.
  *   dQ/dK/dV are fully overwritten (no zero-fill needed).
@@ -118,12 +126,13 @@ int mt_gqa_attn_bwd(const void* q, const void* k, const void* v, const void* o, 
  * process ends.  The dK/dV head split is mt_gqa_attn_bwd's when its partials
  * fit (then the results are bit-identical), else the largest smaller one that
  * fits; a shape whose delta and LSE vectors alone (8 * B * Hq * T bytes,
- * rounded up) exceed the array returns MT_E_WORKSPACE before any device call.
+ * rounded up) exceed the array returns MT_E_WORKSPACE, and an invalid shape
+ * its MT_E_* code, before any device call.
  * Nothing in the array needs to start at zero: every value read was written
  * earlier in the same call.  All calls on one GPU share that GPU's array, so
  * calls that overlap in time on one GPU (other streams, other threads) race;
  * serialise them.  Calls no hipMalloc / hipFree.  The stream, when given,
- * must belong to the current device.
+ * must belong to the current device (else MT_E_DEVICE).
  */
 #define MT_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int mt_gqa_attn_bwd_noalloc(const void* q, const void* k, const void* v, const void* o, const float* lse,

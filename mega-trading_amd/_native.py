@@ -26,6 +26,7 @@ EXPORTS = (
     "mt_version",
     "mt_last_error",
     "mt_gqa_attn_bwd_workspace_size",
+    "mt_gqa_attn_bwd_workspace_size_dtype",
     "mt_gqa_attn_fwd",
     "mt_gqa_attn_bwd",
     "mt_gqa_attn_bwd_dq",
@@ -63,6 +64,7 @@ _FWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P,
 _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]
 _L = ctypes.c_int64
 _OPS_SIGNATURES = {
+    "mt_gqa_attn_bwd_workspace_size_dtype": (_S, [_I, _I, _I, _I, _I, _I]),
     "mt_gqa_attn_bwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]),
     "mt_rms_norm_fwd": (_I, [_P, _L, _P, _P, _P, _L, _I, _F, _I, _I, _P]),
     "mt_add_rms_norm_fwd": (_I, [_P, _L, _P, _L, _P, _P, _P, _P, _L, _I, _F, _I, _I, _P]),

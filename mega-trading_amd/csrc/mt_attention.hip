@@ -146,8 +146,13 @@ size_t workspace_bytes_split(int B, int Hq, int Hkv, int T, int D, int split) {
   return delta_bytes(B, Hq, T) + part;
 }
 
-size_t workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
-  return workspace_bytes_split(B, Hq, Hkv, T, D, choose_split(B, Hq, Hkv, T, D));
+// the fp32 backward kernels never split a key block's heads (no partials)
+int split_for(int B, int Hq, int Hkv, int T, int D, int dtype) {
+  return dtype == MT_DTYPE_FP32 ? 1 : choose_split(B, Hq, Hkv, T, D);
+}
+
+size_t workspace_bytes(int B, int Hq, int Hkv, int T, int D, int dtype) {
+  return workspace_bytes_split(B, Hq, Hkv, T, D, split_for(B, Hq, Hkv, T, D, dtype));
 }
 
 // fwd / dQ workgroup geometry for `pairs` (query head, 64-row block) pairs per
@@ -455,7 +460,7 @@ int bwd_impl(int stage, const void* q, const void* k, const void* v, const void*
   if (!lse) return fail(MT_E_NULL, "lse is NULL");
   if (!workspace) return fail(MT_E_NULL, "workspace is NULL");
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(MT_E_STRIDE, "workspace must be 256-byte aligned");
-  if (split <= 0) split = choose_split(B, Hq, Hkv, T, D);
+  if (split <= 0) split = split_for(B, Hq, Hkv, T, D, dtype);
   const size_t need = workspace_bytes_split(B, Hq, Hkv, T, D, split);
   if (workspace_size < need)
     return fail(MT_E_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", workspace_size, need);
@@ -553,7 +558,12 @@ int mt_time_next_kernel(void* start_event, void* stop_event) {
 
 size_t mt_gqa_attn_bwd_workspace_size(int B, int Hq, int Hkv, int T, int D) {
   if (B < 1 || Hq < 1 || Hkv < 1 || T < 1 || Hq % Hkv) return 0;
-  return workspace_bytes(B, Hq, Hkv, T, D);
+  return workspace_bytes(B, Hq, Hkv, T, D, MT_DTYPE_BF16);  // the 16-bit split: an upper bound for every dtype
+}
+
+size_t mt_gqa_attn_bwd_workspace_size_dtype(int B, int Hq, int Hkv, int T, int D, int dtype) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || T < 1 || Hq % Hkv) return 0;
+  return workspace_bytes(B, Hq, Hkv, T, D, dtype);
 }
 
 int mt_gqa_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, void* q_rot, void* k_rot,
@@ -609,25 +619,26 @@ int mt_gqa_attn_bwd_noalloc(const void* q, const void* k, const void* v, const v
                             const void* dout, void* dq, void* dk, void* dv, int B, int Hq, int Hkv, int T, int D,
                             const int64_t* strides, float scale, int dtype, const float* rope_cos,
                             const float* rope_sin, void* stream) {
-  // shape checks first: a shape that does not fit is rejected before any device call
+  // shape checks first: a shape whose delta / LSE vectors alone do not fit
+  // is rejected before any device call
   int rc = check_common(B, Hq, Hkv, T, D, dtype, rope_cos, rope_sin);
   if (rc) return rc;
-  // the standard head split when its partials fit, else the largest smaller
-  // one that fits (split 1 keeps only delta and LSE)
-  int split = choose_split(B, Hq, Hkv, T, D);
-  while (split > 1 && workspace_bytes_split(B, Hq, Hkv, T, D, split) > MT_NOALLOC_SCRATCH_BYTES) --split;
-  const size_t need = workspace_bytes_split(B, Hq, Hkv, T, D, split);
-  if (need > MT_NOALLOC_SCRATCH_BYTES)
+  const size_t base = workspace_bytes_split(B, Hq, Hkv, T, D, 1);
+  if (base > MT_NOALLOC_SCRATCH_BYTES)
     return fail(MT_E_WORKSPACE,
                 "shape B=%d Hq=%d T=%d needs %zu bytes of backward scratch; the allocation-free backward holds "
                 "at most %zu (use mt_gqa_attn_bwd with a workspace)",
-                B, Hq, T, need, (size_t)MT_NOALLOC_SCRATCH_BYTES);
+                B, Hq, T, base, (size_t)MT_NOALLOC_SCRATCH_BYTES);
   if (stream) {
     int sdev = -1, cur = -1;
     if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) == hipSuccess && hipGetDevice(&cur) == hipSuccess &&
         sdev != cur)
-      return fail(MT_E_SHAPE, "stream belongs to device %d but device %d is current", sdev, cur);
+      return fail(MT_E_DEVICE, "stream belongs to device %d but device %d is current", sdev, cur);
   }
+  // the standard head split when its partials fit, else the largest smaller
+  // one that fits (split 1 keeps only delta and LSE, which fit)
+  int split = split_for(B, Hq, Hkv, T, D, dtype);
+  while (split > 1 && workspace_bytes_split(B, Hq, Hkv, T, D, split) > MT_NOALLOC_SCRATCH_BYTES) --split;
   void* ws = nullptr;
   if ((rc = scratch_address(&ws))) return rc;
   return bwd_impl(3, q, k, v, o, lse, dout, dq, dk, dv, ws, MT_NOALLOC_SCRATCH_BYTES, B, Hq, Hkv, T, D, strides,

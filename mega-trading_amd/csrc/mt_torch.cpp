@@ -65,7 +65,11 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward(
   const c10::DeviceGuard guard(q_in.device());
   const at::Tensor q = ready(q_in), k = ready(k_in), v = ready(v_in);
   const int64_t b = q.size(0), hq = q.size(1), t = q.size(2), d = q.size(3), hkv = k.size(1);
-  if (!out.defined()) out = ready(at::empty_like(q));
+  // the returned output has the query's strides (empty_like of the caller's
+  // q, as the reference allocates it); when those are not kernel-ready the
+  // kernel writes a contiguous buffer that is copied into it afterwards
+  at::Tensor result = out.defined() ? out : at::empty_like(q_in);
+  out = ready(result);
   const at::Tensor lse = at::empty({b, hq, t}, q.options().dtype(at::kFloat));
   const bool rope = cos.has_value() && cos->defined();
   at::Tensor q_rot, k_rot;
@@ -87,7 +91,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward(
                            static_cast<const float*>(ptr_or_null(cos)), static_cast<const float*>(ptr_or_null(sin)),
                            stream_of(q)),
            "mt_gqa_attn_fwd");
-  return {out, lse, q_rot, k_rot};
+  if (!result.is_same(out)) result.copy_(out);
+  return {result, lse, q_rot, k_rot};
 }
 
 // Backward into the given dq / dk / dv (shapes of q / k / v, kernel-ready strides).
@@ -103,7 +108,7 @@ void backward(const at::Tensor& q_in, const at::Tensor& k_in, const at::Tensor& 
   std::array<int64_t, 32> s{};
   const at::Tensor* ts[8] = {&q, &k, &v, &o, &dout, &dq, &dk, &dv};
   for (int i = 0; i < 8; ++i) put_strides(s.data() + 4 * i, *ts[i]);
-  const size_t ws_bytes = mt_gqa_attn_bwd_workspace_size(int(b), int(hq), int(hkv), int(t), int(d));
+  const size_t ws_bytes = mt_gqa_attn_bwd_workspace_size_dtype(int(b), int(hq), int(hkv), int(t), int(d), dtype_code(q));
   const at::Tensor ws = at::empty({int64_t(ws_bytes)}, q.options().dtype(at::kByte));
   check_rc(mt_gqa_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr<float>(),
                            dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,

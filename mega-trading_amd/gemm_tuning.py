@@ -10,8 +10,12 @@ itself off, and restores the process-wide TunableOp state afterwards, so
 GEMMs outside this package (and the baseline routes the benchmark compares
 against) keep the default selection.
 
-The recorded choices live in ``tuned/gemm_gfx950.csv``, written by
-``python -m mega-trading_amd.tune_gemms`` on the target GPU.  TunableOp checks
+The recorded choices live in ``tuned/gemm_gfx950.csv``.  They were recorded
+on an MI355X by running the "hip" route's C5 train step (two steps, bf16
+autocast) and its eager cached decode (fp32, 32 rows, two tokens) with
+``_state["tuning"] = True`` and ``torch.cuda.tunable.set_filename(<csv>)``,
+so TunableOp tuned exactly the GEMMs opened inside ``tuned_gemms()`` and
+wrote the file at process exit.  TunableOp checks
 the file's validators (PyTorch, HIP, hipBLASLt and rocBLAS versions, GPU
 architecture) and ignores a file that does not match, in which case the
 default selection runs: the file only ever changes which library kernel

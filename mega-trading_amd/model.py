@@ -63,6 +63,15 @@ __all__ = ["TradingModel", "LlamaDecoderBlock", "LlamaAttention", "SwiGLU", "RMS
 
 ATTENTION_BACKENDS = ("auto", "flash", "efficient", "math", "triton", "hip")
 HIP_BACKENDS = ("triton", "hip")
+_KERNEL_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _kernel_operands(*tensors: torch.Tensor) -> bool:
+    """The operator kernels' precondition, as the reference's ``_can_use_triton``
+    (``triton_ops.py:95-96``): GPU tensors of a 16- or 32-bit float dtype.  Where
+    it fails the reference's triton_* operators compute with torch instead, and
+    so do the operator routes here (the attention op itself has no such path)."""
+    return all(t.is_cuda and t.dtype in _KERNEL_DTYPES for t in tensors)
 
 
 class TradingModel(nn.Module):
@@ -140,10 +149,16 @@ class TradingModel(nn.Module):
         if labels.shape != input_ids.shape:
             raise ValueError("labels must match input_ids shape")
         normalized = self._hidden(input_ids)
-        if self.operator_backend in HIP_BACKENDS and not return_logits:
+        if self.operator_backend in HIP_BACKENDS and not return_logits and _kernel_operands(normalized,
+                                                                                           self.output.weight):
             loss = _hip_fused_linear_cross_entropy(normalized.reshape(-1, normalized.shape[-1]), self.output.weight,
                                                    labels.reshape(-1), ignore_index=ignore_index)
             return loss, None
+        if self.operator_backend in HIP_BACKENDS and not return_logits and not bool((labels != ignore_index).any()):
+            # the reference's torch form of the fused loss returns a zero loss
+            # when every label is ignored, where F.cross_entropy gives NaN
+            # (triton_ops.py:107-110)
+            return (normalized.sum() + self.output.weight.sum()) * 0.0, None
         logits = self.output(normalized)
         loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), labels.reshape(-1), ignore_index=ignore_index)
         return loss, (logits if return_logits else None)
@@ -462,7 +477,7 @@ class SwiGLU(nn.Module):
             return _project_packed(self.dropout(gated), (self.w2.weight,))
         gate = self.w1(hidden)
         up = self.w3(hidden)
-        if self.operator_backend in HIP_BACKENDS:
+        if self.operator_backend in HIP_BACKENDS and _kernel_operands(gate, up) and gate.shape == up.shape:
             gated = _hip_swiglu_gate(gate, up)
         else:
             gated = F.silu(gate) * up
@@ -514,7 +529,11 @@ class RotaryEmbedding(nn.Module):
             raise ValueError(f"sequence length {sequence_length} exceeds RoPE cache length {self.cos.shape[-2]}")
         cos = self.cos[:, :, :sequence_length].to(dtype=query.dtype)
         sin = self.sin[:, :, :sequence_length].to(dtype=query.dtype)
-        if self.operator_backend in HIP_BACKENDS:
+        # the reference's triton_apply_rope computes with torch for tensors its
+        # kernel does not take, and when query and key differ in head size
+        # (triton_ops.py:51-52)
+        if (self.operator_backend in HIP_BACKENDS and _kernel_operands(query, key)
+                and query.shape[-1] == key.shape[-1]):
             return _hip_apply_rope(query, key, cos, sin)
         return rotate(query, cos, sin), rotate(key, cos, sin)
 

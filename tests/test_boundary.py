@@ -192,6 +192,30 @@ def test_c_abi_rejects_bad_arguments_before_launch(mta):
         assert fn(p, p, p, p, p, p, p, p, p, p, need, 1, 4, 2, 16, 33, arr, 0.125, 0, None, None, None) == E_SHAPE
 
 
+def test_bwd_workspace_size_per_dtype(mta):
+    """The fp32 backward never splits a key block's heads, so it needs only the
+    delta / LSE vectors; the 16-bit backward of a group of 8 heads with a single
+    key block splits them and needs the fp32 partials too.  The dtype-free size
+    query is the upper bound (the 16-bit size), and mt_gqa_attn_bwd checks the
+    given workspace against its dtype's exact size."""
+    lib = mta._native.load()
+    b, hq, hkv, t, d = 1, 8, 1, 64, 64
+    vec = (b * hq * t * 4 + 255) // 256 * 256
+    f32 = lib.mt_gqa_attn_bwd_workspace_size_dtype(b, hq, hkv, t, d, 2)
+    bf16 = lib.mt_gqa_attn_bwd_workspace_size_dtype(b, hq, hkv, t, d, 0)
+    assert f32 == 2 * vec
+    assert bf16 > f32 and bf16 == lib.mt_gqa_attn_bwd_workspace_size(b, hq, hkv, t, d)
+    assert lib.mt_gqa_attn_bwd_workspace_size_dtype(b, 5, 2, t, d, 2) == 0
+    # a workspace of exactly the fp32 size passes the size check (the call then
+    # stops at the deliberately bad q stride, before any device work); one byte
+    # less is MT_E_WORKSPACE
+    p = 0x1000
+    arr = (ctypes.c_int64 * 32)(*([0, 0, 64, 2] + [0, 0, 64, 1] * 7))
+    args = (b, hq, hkv, t, d, arr, 0.125, 2, None, None, None)
+    assert lib.mt_gqa_attn_bwd(p, p, p, p, p, p, p, p, p, p, f32, *args) == -3  # MT_E_STRIDE
+    assert lib.mt_gqa_attn_bwd(p, p, p, p, p, p, p, p, p, p, f32 - 1, *args) == -6
+
+
 def test_error_codes_raise_python_errors(mta):
     with pytest.raises(mta._native.HipAttentionError, match="head_dim"):
         mta._native.check(_fwd_call(mta._native.load(), d=40), "mt_gqa_attn_fwd")

@@ -50,6 +50,7 @@ def test_hip_backend_calls_local_kernel(backend):
     # the RoPE kernel stand-in rotates in torch, so the attention sees rotated q / k
     with patch("mega-trading_amd.model._hip_apply_rope",
                side_effect=lambda q, k, c, s: (rotate(q, c, s), rotate(k, c, s))) as rope_op, \
+            patch("mega-trading_amd.model._kernel_operands", return_value=True), \
             patch("mega-trading_amd.model._hip_attention", return_value=torch.zeros(1, 4, 8, 4)) as op:
         out = attention(hidden)
     rope_op.assert_called_once()
@@ -68,7 +69,8 @@ def test_rotary_embedding_routes_by_operator_backend(backend, kernel):
     # as the reference test patches _triton_apply_rope (tests/test_training.py:470-475)
     rope = RotaryEmbedding(head_dim=4, max_sequence_length=8, theta=10_000.0, operator_backend=backend)
     query, key = torch.randn(1, 4, 8, 4), torch.randn(1, 2, 8, 4)
-    with patch("mega-trading_amd.model._hip_apply_rope", return_value=(query, key)) as rope_kernel:
+    with patch("mega-trading_amd.model._hip_apply_rope", return_value=(query, key)) as rope_kernel, \
+            patch("mega-trading_amd.model._kernel_operands", return_value=True):
         out_q, _out_k = rope(query, key)
     assert rope_kernel.call_count == (1 if kernel else 0)
     assert out_q.shape == query.shape
@@ -120,6 +122,7 @@ def test_dropout_in_training_falls_back_to_sdpa():
     hidden = torch.randn(1, 8, 16)
     with patch("mega-trading_amd.model.F.scaled_dot_product_attention", return_value=torch.zeros(1, 4, 8, 4)) as sdpa, \
             patch("mega-trading_amd.model._hip_rope_attention") as op, \
+            patch("mega-trading_amd.model._kernel_operands", return_value=True), \
             patch("mega-trading_amd.model._hip_apply_rope", side_effect=lambda q, k, c, s: (q, k)) as rope_op:
         attention(hidden)
     assert sdpa.call_args.kwargs["dropout_p"] == 0.1
@@ -177,6 +180,35 @@ def test_model_forward_shapes_and_errors():
         m(torch.randint(0, 32, (8,)))
 
 
+def test_triton_operators_compute_with_torch_where_the_reference_does():
+    # triton_ops.py:51-52, 59-60, 87-88: the reference's triton_* operators take
+    # torch's path for tensors their kernels do not take (here: CPU tensors, as in
+    # a "triton" model training with dropout > 0 on the CPU), so the same model
+    # runs here and equals the "auto" model with the same weights
+    kw = dict(vocab_size=32, block_size=8, hidden_dim=16, layers=1, attention_heads=4, kv_heads=2, dropout=0.1,
+              rope_theta=10_000.0)
+    tri = model_mod.TradingModel(attention_backend="triton", **kw)
+    ref = model_mod.TradingModel(attention_backend="auto", **kw)
+    ref.load_state_dict(tri.state_dict())
+    ids = torch.randint(0, 32, (2, 8))
+    for m in (tri, ref):
+        m.train()
+    torch.manual_seed(3)
+    loss_t, _ = tri.forward_with_loss(ids, ids, return_logits=False)
+    torch.manual_seed(3)
+    loss_r, _ = ref.forward_with_loss(ids, ids, return_logits=False)
+    torch.testing.assert_close(loss_t, loss_r)
+    rope = RotaryEmbedding(head_dim=4, max_sequence_length=8, theta=10_000.0, operator_backend="triton")
+    q, k = torch.randn(1, 4, 8, 4, dtype=torch.float64), torch.randn(1, 2, 8, 4, dtype=torch.float64)
+    cos, sin = rope.cos.to(torch.float64), rope.sin.to(torch.float64)
+    rq, rk = rope(q, k)
+    torch.testing.assert_close(rq, rotate(q, cos, sin))
+    torch.testing.assert_close(rk, rotate(k, cos, sin))
+    # every label ignored: a zero loss (the reference's torch form of the fused loss), not NaN
+    loss0, _ = tri.forward_with_loss(ids, torch.full_like(ids, -100), return_logits=False)
+    assert float(loss0.detach()) == 0.0
+
+
 def test_hip_route_on_cpu_tensors_raises():
     m = model_mod.TradingModel(vocab_size=32, block_size=8, hidden_dim=256, layers=1, attention_heads=4, kv_heads=2,
                                dropout=0.0, rope_theta=10_000.0, attention_backend="hip")
@@ -211,6 +243,7 @@ def test_operator_routing_follows_the_reference(backend, gate, norm_hip):
     ffn = m.blocks[0].feed_forward
     ref = ffn.w2(F.silu(ffn.w1(hidden)) * ffn.w3(hidden))
     with patch("mega-trading_amd.model._hip_swiglu_gate", side_effect=lambda g, u: F.silu(g) * u) as pair, \
+         patch("mega-trading_amd.model._kernel_operands", return_value=True), \
          patch("mega-trading_amd.model._hip_swiglu_gate_packed",
                side_effect=lambda gu: F.silu(gu[..., :gu.shape[-1] // 2]) * gu[..., gu.shape[-1] // 2:]) as packed:
         out = ffn(hidden)
@@ -232,7 +265,8 @@ def test_loss_head_routing(backend, fused):
                                dropout=0.0, rope_theta=10_000.0, attention_backend="auto")
     m.operator_backend = backend  # keep the rest of the network on torch ops (CPU)
     ids = torch.randint(0, 32, (2, 8))
-    with patch("mega-trading_amd.model._hip_fused_linear_cross_entropy", return_value=torch.tensor(1.5)) as ce:
+    with patch("mega-trading_amd.model._hip_fused_linear_cross_entropy", return_value=torch.tensor(1.5)) as ce, \
+            patch("mega-trading_amd.model._kernel_operands", return_value=True):
         loss, logits = m.forward_with_loss(ids, ids, return_logits=False)
     assert ce.called == fused and logits is None
     if fused:
