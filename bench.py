@@ -290,6 +290,81 @@ def time_ops(pkg, iters=20):
     return res
 
 
+DECODE_SHAPE = (32, 8, 2, 64, 1024)  # C5 generation: rollouts, Hq, Hkv, D, cache capacity (block_size)
+
+
+def time_decode(pkg, lengths=(544, 1024), iters=50):
+    """One decode step's attention kernels at the config 5 generation shape
+    (32 rollouts, Hq 8, Hkv 2, D 64, a 1024-position bf16 cache), through the
+    C ABI with preallocated buffers, the length read from device memory as the
+    recorded decode step does: the split + combine pair (mt_gqa_attn_decode_dev)
+    and the RoPE / cache-append kernel, each timed over `iters` back-to-back
+    launches with HIP events.  Algorithmic bytes: the split kernel reads the
+    group's q and L cached K and V rows once and writes one fp32 partial
+    (o, m, l) per 64-key split; the combine reads the partials and writes O;
+    the append reads the fp32 q / k / v projections and writes q_rot and one
+    K and one V cache row."""
+    native = pkg._native
+    lib = native.load()
+    dev = torch.device("cuda:0")
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    b, hq, hkv, d, cap = DECODE_SHAPE
+    g = torch.Generator(device=dev).manual_seed(0)
+    kc = (torch.randn(b, hkv, cap, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    vc = (torch.randn(b, hkv, cap, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    q = (torch.randn(b, hq, 1, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ws_bytes = lib.mt_gqa_attn_decode_workspace_size(b, hq, cap, d)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    st = native.strides_array(q, kc, vc, out)
+    length = torch.zeros(1, device=dev, dtype=torch.int32)
+    # fp32 projections of the new token (generation runs the fp32 model), RoPE tables [cap, D/2]
+    xq = torch.randn(b, hq, 1, d, device=dev, generator=g)
+    xk = torch.randn(b, hkv, 1, d, device=dev, generator=g)
+    xv = torch.randn(b, hkv, 1, d, device=dev, generator=g)
+    cos, sin = rope_tables(cap, d, 10_000.0, dev)
+    q_rot = torch.empty_like(q)
+    ins = (ctypes.c_int64 * 6)(xq.stride(0), xq.stride(1), xk.stride(0), xk.stride(1), xv.stride(0), xv.stride(1))
+    cst = (ctypes.c_int64 * 6)(*kc.stride()[:3], *vc.stride()[:3])
+    scale = 1.0 / math.sqrt(d)
+    res = {}
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    for L in lengths:
+        length.fill_(L)
+        ns = (L + 63) // 64
+        attn = lambda: native.check(lib.mt_gqa_attn_decode_dev(  # noqa: E731
+            q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), b, hq, hkv, cap, length.data_ptr(), d, st,
+            scale, native.DTYPE_BF16, ws.data_ptr(), ws_bytes, sp), "mt_gqa_attn_decode_dev")
+        append = lambda: native.check(lib.mt_decode_rope_append(  # noqa: E731
+            xq.data_ptr(), xk.data_ptr(), xv.data_ptr(), ins, cos.data_ptr(), sin.data_ptr(), cap, L - 1, None,
+            q_rot.data_ptr(), kc.data_ptr(), vc.data_ptr(), cst, cap, b, hq, hkv, d, native.DTYPE_FP32,
+            native.DTYPE_BF16, sp), "mt_decode_rope_append")
+        kv_bytes = 2 * b * hkv * L * d * 2
+        part_bytes = b * hq * ns * (d + 2) * 4
+        split_bytes = kv_bytes + b * hq * d * 2 + part_bytes
+        comb_bytes = part_bytes + b * hq * d * 2
+        us = timed(attn, iters)
+        us_app = timed(append, iters)
+        app_bytes = b * (hq + 2 * hkv) * d * 4 + b * (hq + 2 * hkv) * d * 2 + d * 4
+        res[f"L{L}"] = {"attention_us": round(us, 2), "split_bytes": split_bytes, "combine_bytes": comb_bytes,
+                        "attention_GBps": round((split_bytes + comb_bytes) / (us * 1e-6) / 1e9, 1),
+                        "rope_append_us": round(us_app, 2), "rope_append_bytes": app_bytes}
+    res["shape"] = "B=32 Hq=8 Hkv=2 D=64 bf16 cache of 1024 positions, length from device memory"
+    return res
+
+
 def time_kernels(pkg, cfg, iters):
     """Average duration of each main kernel (HIP events the library records
     around it on its launch stream, one pair per launch) and of each whole
@@ -687,8 +762,14 @@ def main(argv=None) -> int:
                     help="profiling driver: run only the decoder operators' kernels at config 5 shapes, then a "
                          "256 MiB device copy (counter calibration), and print their timings")
     ap.add_argument("--kernels-only", action="store_true",
-                    help="profiling driver: run only the C3 kernels stage by stage, then a 256 MiB device copy "
-                         "(the reference kernel for HBM-traffic counter calibration), and print their timings")
+                    help="profiling driver: run only the attention kernels of one config (--config, default C3) "
+                         "stage by stage, then a 256 MiB device copy (the reference kernel for HBM-traffic counter "
+                         "calibration), and print their timings")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="profiling driver: run only the decode step's attention kernels at the config 5 generation "
+                         "shape, then a 256 MiB device copy (counter calibration), and print their timings")
+    ap.add_argument("--config", choices=("C2", "C3", "C4"), default="C3",
+                    help="BASELINE config that --kernels-only runs")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path is single-GPU; got --gpus {args.gpus})", file=sys.stderr)
@@ -705,8 +786,14 @@ def main(argv=None) -> int:
         print(json.dumps({"ops": ops_res, "copy_bytes_each_way": 256 << 20}), flush=True)
         return 0
 
+    if args.decode_only:
+        dec = time_decode(pkg)
+        _calibration_copy()
+        print(json.dumps({"decode": dec, "copy_bytes_each_way": 256 << 20}), flush=True)
+        return 0
+
     if args.kernels_only:
-        kern = time_kernels(pkg, C3, args.steps)
+        kern = time_kernels(pkg, {"C2": C2, "C3": C3, "C4": C4}[args.config], args.steps)
         _calibration_copy()
         print(json.dumps({"kernels": kern, "copy_bytes_each_way": 256 << 20}), flush=True)
         return 0
@@ -728,6 +815,7 @@ def main(argv=None) -> int:
     ms_c4 = time_op_steps(pkg, C4, max(10, args.steps // 2), 3, rope=True)["ms"]
     ceiling = mfma_ceiling()
     ops_line = time_ops(pkg)
+    decode_line = time_decode(pkg)
 
     line = {
         "metric": METRIC,
@@ -769,6 +857,7 @@ def main(argv=None) -> int:
                     for n, x in kern.items()},
         "mfma_ceiling": ceiling,
         "ops": ops_line,
+        "decode": decode_line,
         "secondary": {
             "C2_fwd_bwd_tflops": round(fwd_bwd_flops(*C2[:1], C2[1], C2[2], C2[4]) / (ms_c2 * 1e-3) / 1e12, 2),
             "C2_ms_per_step": round(ms_c2, 4),
