@@ -183,8 +183,8 @@ int mt_time_next_kernel(void* start_event, void* stop_event);
  *   q [B,Hq,1,D] (rotated if RoPE is used), k_cache / v_cache [B,Hkv,>=L,D]
  *   (rotated keys), o [B,Hq,1,D] written; strides: 16 int64 = q, k_cache,
  *   v_cache, o in (b, h, t, d) order (the t stride of q and o is unused).
- *   Hq / Hkv <= 8; L >= 1.  The fp32 workspace holds per-split partials
- *   (mt_gqa_attn_decode_workspace_size).
+ *   Hq / Hkv <= 8; L >= 1.  The fp32 workspace (16-byte aligned) holds one
+ *   partial per 64-key split (mt_gqa_attn_decode_workspace_size).
  */
 size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D);
 int mt_gqa_attn_decode(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv,

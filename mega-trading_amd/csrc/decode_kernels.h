@@ -4,28 +4,37 @@
 // instead; the maths is the causal GQA attention of triton_attention.py for the
 // last query row, whose keys are all cached positions).
 //
-// Split-K ("flash decoding"): the cached keys 0..L-1 are cut into 256-key
-// splits; workgroup (batch, KV head, split) scores its split for all R query
-// heads of the KV group (each K/V row is read once for the R heads), forms the
-// split's softmax numerator and running offset, and writes an fp32 partial
-// (o, m, l).  A second kernel merges the splits with the log-sum-exp rule.
-// The work is HBM-bound (the cache is read once), so it uses plain fp32 FMAs:
-// with one query row per head there is no matrix product to feed the MFMAs.
+// Split-K ("flash decoding"): the cached keys 0..L-1 are cut into 64-key
+// splits and each split is one wave (workgroup (batch, KV head, split)).  The
+// wave scores its split for all R query heads of the KV group (each K/V row is
+// read once for the R heads), forms the split's softmax numerator and offset,
+// and writes an fp32 partial (o, m, l).  A second kernel merges the splits
+// with the log-sum-exp rule.  The work is HBM- and latency-bound (the cache is
+// read once; at the decoder's shapes a split's data is a few KB), so it uses
+// plain fp32 FMAs -- with one query row per head there is no matrix product to
+// feed the MFMAs -- and is laid out for few dependent steps: every K and V
+// load of a lane is issued at entry, the reductions stay inside the wave (DPP
+// within 16-lane rows, permlane swaps across rows), and one LDS exchange hands
+// the probabilities from the score layout (lane = key) to the V layout.
 #pragma once
 
 #include "mt_common.h"
 
 namespace mt {
 
-constexpr int kDecSplit = 256;  // keys per split (one per thread in the score pass)
+constexpr int kDecSplit = 64;   // keys per split: one wave, one key per lane in the score pass
 constexpr int kDecMaxR = 8;     // query heads per KV head supported
+
+// fp32 floats per partial: o[0..D), m (log2), l, two pad floats (16-byte rows)
+template <int D>
+constexpr int dec_row() { return D + 4; }
 
 struct DecodeParams {
   const uint16_t* q;  // [B, Hq, 1, D] (rotated when RoPE is used)
   const uint16_t* k;  // [B, Hkv, >= L, D] cache (rotated keys)
   const uint16_t* v;  // [B, Hkv, >= L, D] cache
   uint16_t* out;      // [B, Hq, 1, D]
-  float* part;        // [B, Hq, nsplit, D + 2] fp32: o (unnormalised), m (log2), l
+  float* part;        // [B, Hq, nsplit, D + 4] fp32: o (unnormalised), m (log2), l
   int64_t sq[2], sk[3], sv[3], so[2];  // strides (b, h) for q / o, (b, h, t) for the caches
   const int* length_dev;  // when set, L is read from device memory (graph-replayable decode)
   int B, Hq, Hkv, R, L, nsplit;  // nsplit: splits in the grid (of the capacity when length_dev is set)
@@ -37,172 +46,201 @@ __device__ __forceinline__ int decode_length(const DecodeParams& p) {
   return p.length_dev ? min(max(*p.length_dev, 1), p.L) : p.L;
 }
 
-template <class E, int D>
-__global__ __launch_bounds__(256) void attn_decode_split_kernel(DecodeParams p) {
-  __shared__ float qs[kDecMaxR][D];
-  __shared__ float ps[kDecMaxR][kDecSplit];
-  __shared__ float red[kDecMaxR][4];
-  __shared__ float red_buf[(256 / (D / 8)) * kDecMaxR * D];  // V-pass key-group sums (64 KB)
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <bool MAX>
+__device__ __forceinline__ float red_op(float a, float b) {
+  return MAX ? fmaxf(a, b) : a + b;
+}
+
+// Max or sum over lane bits [LO, 6) of a wave64; every lane receives the
+// result.  Bits 0-1: quad permutations; bits 2-3: row rotations by 4 and 8
+// (after them each lane holds the sum over the lanes of its row that agree
+// with it in the lower bits); bits 4-5: v_permlane16/32_swap.
+template <int LO, bool MAX>
+__device__ __forceinline__ float wave_reduce(float x) {
+  if constexpr (LO <= 0) x = red_op<MAX>(x, dpp_mov<0xB1>(x));   // quad_perm(1,0,3,2): lane ^ 1
+  if constexpr (LO <= 1) x = red_op<MAX>(x, dpp_mov<0x4E>(x));   // quad_perm(2,3,0,1): lane ^ 2
+  if constexpr (LO <= 2) x = red_op<MAX>(x, dpp_mov<0x124>(x));  // row_ror:4
+  if constexpr (LO <= 3) x = red_op<MAX>(x, dpp_mov<0x128>(x));  // row_ror:8
+  if constexpr (LO <= 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// R (query heads of the KV group) is a template parameter: the per-head loops
+// then unroll into straight-line code whose LDS reads issue back to back (with
+// a run-time R every head is a branch with its own wait on its reads).
+template <class E, int D, int R>
+__global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeParams p) {
+  static_assert(D == 32 || D == 64 || D == 128, "head size");
+  static_assert(R >= 1 && R <= kDecMaxR, "group size");
+  constexpr int NC = D / 8;                 // 16-byte chunks per row
+  constexpr int G = 64 / NC;                // key groups of the V pass
+  constexpr int NV = kDecSplit / G;         // V chunks per lane
+  constexpr int LO = NC == 4 ? 2 : NC == 8 ? 3 : 4;  // log2(NC): lane bits of the d chunk
+  __shared__ f32x4 qs[R][D / 4];
+  __shared__ float ps[R][kDecSplit];
+  const int lane = threadIdx.x;
   const int s = blockIdx.x % p.nsplit;
   const int g = blockIdx.x / p.nsplit;
   const int kvh = g % p.Hkv;
   const int b = g / p.Hkv;
-  const int R = p.R;
   const int k0 = s * kDecSplit;
   const int L = decode_length(p);
   if (k0 >= L) return;  // a split past the current length (device-length launches cover the capacity)
   const int n = min(kDecSplit, L - k0);
 
-  // Every K and V load of this thread is issued first, so the score, softmax
-  // and V passes wait on one memory round trip: the K row of key k0 + tid,
-  // and the 16-byte V chunks of the V pass (chunk c = tid % NC of keys
-  // tid / NC, tid / NC + G, ...).
-  constexpr int NC = D / 8;      // 16-byte chunks per V row
-  constexpr int G = 256 / NC;    // key groups of the V pass
-  constexpr int NV = kDecSplit / G;  // V chunks per thread
-  u32x4 kw[D / 8], vw[NV];
-  if (tid < n) {
-    const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + tid) * p.sk[2];
+  // Every K and V load first (one memory round trip).  Score layout: lane =
+  // key k0 + lane.  V layout: lane = (d chunk c = lane % NC, key group
+  // lane / NC), keys j = lane / NC + i G.  Keys past the split's end load its
+  // last key instead (in bounds; their probabilities are zero).
+  const int c = lane % NC;
+  const int kg = lane / NC;
+  u32x4 kw[NC], vw[NV];
+  {
+    const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + min(lane, n - 1)) * p.sk[2];
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c) kw[c] = *reinterpret_cast<const u32x4*>(krow + 8 * c);
+    for (int cc = 0; cc < NC; ++cc) kw[cc] = *reinterpret_cast<const u32x4*>(krow + 8 * cc);
+    const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2] + 8 * c;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      vw[i] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)min(kg + i * G, n - 1) * p.sv[2]);
   }
-  const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2];
-  const int c = tid % NC;
+  // the group's R query rows, as fp32 in LDS (read back as broadcasts)
+  {
+    const uint16_t* qb = p.q + b * p.sq[0] + (int64_t)(kvh * R) * p.sq[1];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = tid / NC + i * G;
-    if (j < n) vw[i] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)j * p.sv[2] + 8 * c);
-  }
-
-  for (int i = tid; i < R * D; i += 256) {
-    const int h = i / D, d = i % D;
-    qs[h][d] = E::to_f(p.q[b * p.sq[0] + (int64_t)(kvh * R + h) * p.sq[1] + d]);
-  }
-  __syncthreads();
-
-  // scores of key k0 + tid for every head (log2 units)
-  float sc[kDecMaxR];
-#pragma unroll
-  for (int h = 0; h < kDecMaxR; ++h) sc[h] = 0.f;
-  if (tid < n) {
-#pragma unroll
-    for (int c8 = 0; c8 < D / 8; ++c8) {
-      const u32x4 w = kw[c8];
-      float kv[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kv[2 * e] = lo_f<E>(w[e]);
-        kv[2 * e + 1] = hi_f<E>(w[e]);
+    for (int i0 = 0; i0 < R * NC; i0 += 64) {
+      const int i = i0 + lane;
+      if (i < R * NC) {
+        const int h = i / NC, cc = i % NC;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(qb + (int64_t)h * p.sq[1] + 8 * cc);
+        qs[h][2 * cc] = f32x4{lo_f<E>(w[0]), hi_f<E>(w[0]), lo_f<E>(w[1]), hi_f<E>(w[1])};
+        qs[h][2 * cc + 1] = f32x4{lo_f<E>(w[2]), hi_f<E>(w[2]), lo_f<E>(w[3]), hi_f<E>(w[3])};
       }
-#pragma unroll
-      for (int h = 0; h < kDecMaxR; ++h)
-        if (h < R)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sc[h] = __builtin_fmaf(qs[h][8 * c8 + e], kv[e], sc[h]);
     }
   }
-  // per-head max over the split
-#pragma unroll
-  for (int h = 0; h < kDecMaxR; ++h) {
-    if (h >= R) break;
-    float v = tid < n ? sc[h] * p.scale_log2 : -INFINITY;
-    sc[h] = v;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    if (lane == 0) red[h][wave] = v;
-  }
   __syncthreads();
-  float m[kDecMaxR];
+
+  // scores of key k0 + lane for every head (log2 units), the split's per-head
+  // offset m and probability sum l
+  float sc[R];
 #pragma unroll
-  for (int h = 0; h < kDecMaxR; ++h)
-    m[h] = h < R ? fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3])) : 0.f;
-  __syncthreads();  // red is reused for the sums
-  // probabilities (0 past the split's last key) and their per-head sums
+  for (int h = 0; h < R; ++h) sc[h] = 0.f;
 #pragma unroll
-  for (int h = 0; h < kDecMaxR; ++h) {
-    if (h >= R) break;
-    const float e = tid < n ? exp2_fast(sc[h] - m[h]) : 0.f;
-    ps[h][tid] = e;
-    float v = e;
+  for (int cc = 0; cc < NC; ++cc) {
+    float kv[8];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) red[h][wave] = v;
+    for (int e = 0; e < 4; ++e) {
+      kv[2 * e] = lo_f<E>(kw[cc][e]);
+      kv[2 * e + 1] = hi_f<E>(kw[cc][e]);
+    }
+#pragma unroll
+    for (int h = 0; h < R; ++h) {
+      const f32x4 q0 = qs[h][2 * cc], q1 = qs[h][2 * cc + 1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[h] = __builtin_fmaf(q0[e], kv[e], sc[h]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[h] = __builtin_fmaf(q1[e], kv[4 + e], sc[h]);
+    }
+  }
+  const bool live = lane < n;
+  float m[R], l[R];
+#pragma unroll
+  for (int h = 0; h < R; ++h) {
+    const float x = live ? sc[h] * p.scale_log2 : -INFINITY;
+    m[h] = wave_reduce<0, true>(x);  // lane 0 is always live: finite
+    const float e = live ? exp2_fast(x - m[h]) : 0.f;
+    ps[h][lane] = e;
+    l[h] = wave_reduce<0, false>(e);
   }
   __syncthreads();
 
-  // o[h][d] = sum_j p[h][j] V[k0 + j][d].  Thread t takes the 8-value d chunk
-  // c = t % NC of keys j = t / NC, t / NC + G, ... (one 16-byte load per key,
-  // issued at the start, feeds 8 d values of every head), then the G key
-  // groups are summed through LDS.
-  float acc[kDecMaxR][8];
+  // o[h][d] = sum_j p[h][j] V[k0 + j][d]: lane (c, kg) sums its NV keys for the
+  // 8 d values of chunk c, then the G key groups are summed across lanes
+  float acc[R][8];
 #pragma unroll
-  for (int h = 0; h < kDecMaxR; ++h)
+  for (int h = 0; h < R; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int j = tid / NC + i * G;
-    if (j >= n) break;
-    const u32x4 w = vw[i];
+    const int j = kg + i * G;
     float vv[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vv[2 * e] = lo_f<E>(w[e]);
-      vv[2 * e + 1] = hi_f<E>(w[e]);
+      vv[2 * e] = lo_f<E>(vw[i][e]);
+      vv[2 * e + 1] = hi_f<E>(vw[i][e]);
     }
 #pragma unroll
-    for (int h = 0; h < kDecMaxR; ++h) {
-      if (h < R) {
-        const float pj = ps[h][j];
+    for (int h = 0; h < R; ++h) {
+      const float pj = ps[h][j];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(pj, vv[e], acc[h][e]);
-      }
+      for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(pj, vv[e], acc[h][e]);
     }
   }
-  // key-group partial sums: red_o[g][h][d]
-  float* red_o = red_buf;
-  const int kg = tid / NC;
 #pragma unroll
-  for (int h = 0; h < kDecMaxR; ++h)
-    if (h < R)
+  for (int h = 0; h < R; ++h)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red_o[(kg * kDecMaxR + h) * D + 8 * c + e] = acc[h][e];
-  __syncthreads();
-  for (int i = tid; i < R * D; i += 256) {
-    const int h = i / D, d = i % D;
-    float o = 0.f;
-#pragma unroll 8
-    for (int gg = 0; gg < G; ++gg) o += red_o[(gg * kDecMaxR + h) * D + d];
-    float* dst = p.part + (((int64_t)b * p.Hq + kvh * R + h) * p.nsplit + s) * (D + 2);
-    dst[d] = o;
-    if (d == 0) {
-      dst[D] = m[h];
-      dst[D + 1] = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+    for (int e = 0; e < 8; ++e) acc[h][e] = wave_reduce<LO, false>(acc[h][e]);
+  if (kg == 0) {
+#pragma unroll
+    for (int h = 0; h < R; ++h) {
+      float* dst = p.part + (((int64_t)b * p.Hq + kvh * R + h) * p.nsplit + s) * dec_row<D>();
+      *reinterpret_cast<f32x4*>(dst + 8 * c) = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+      *reinterpret_cast<f32x4*>(dst + 8 * c + 4) = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+      if (c == 0) *reinterpret_cast<f32x2*>(dst + D) = f32x2{m[h], l[h]};
     }
   }
 }
 
 // Merge the splits of each (batch, query head): M = max m_s,
-// O = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.  One thread per d value.
+// O = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.  One thread per d value;
+// the splits are read 16 at a time with every load of a batch issued before
+// its first use (one memory round trip per 16 splits).
 template <class E, int D>
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(DecodeParams p) {
   constexpr int PER = 256 / D;  // (batch, head) pairs per workgroup
+  constexpr int ROW = dec_row<D>();
+  constexpr int BATCH = 16;
   const int pair = blockIdx.x * PER + threadIdx.x / D;
   const int d = threadIdx.x % D;
   if (pair >= p.B * p.Hq) return;
   const int b = pair / p.Hq, h = pair % p.Hq;
-  const float* src = p.part + (int64_t)pair * p.nsplit * (D + 2);
+  const float* src = p.part + (int64_t)pair * p.nsplit * ROW;
   const int ns = (decode_length(p) + kDecSplit - 1) / kDecSplit;  // splits holding keys
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, src[s * (D + 2) + D]);
-  float o = 0.f, l = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const float w = exp2_fast(src[s * (D + 2) + D] - M);
-    o = __builtin_fmaf(w, src[s * (D + 2) + d], o);
-    l = __builtin_fmaf(w, src[s * (D + 2) + D + 1], l);
+  float M = -INFINITY, o = 0.f, l = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += BATCH) {
+    float ms[BATCH], os[BATCH], ls[BATCH];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const bool in = s0 + i < ns;
+      const float* r = src + (int64_t)(in ? s0 + i : 0) * ROW;
+      const f32x2 ml = *reinterpret_cast<const f32x2*>(r + D);
+      ms[i] = in ? ml[0] : -INFINITY;
+      ls[i] = in ? ml[1] : 0.f;
+      os[i] = in ? r[d] : 0.f;
+    }
+    float mn = M;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) mn = fmaxf(mn, ms[i]);
+    const float a = exp2_fast(M - mn);  // 0 on the first batch (M = -inf)
+    o *= a;
+    l *= a;
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const float w = exp2_fast(ms[i] - mn);
+      o = __builtin_fmaf(w, os[i], o);
+      l = __builtin_fmaf(w, ls[i], l);
+    }
+    M = mn;
   }
   const float r = o / l;
   p.out[b * p.so[0] + (int64_t)h * p.so[1] + d] = uint16_t(pack2<E>(r, 0.f) & 0xffffu);

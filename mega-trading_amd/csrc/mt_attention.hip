@@ -650,7 +650,7 @@ int mt_gqa_attn_bwd_dkv(MT_BWD_ARGS) { return bwd_impl(2, MT_BWD_PASS); }
 size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D) {
   if (B < 1 || Hq < 1 || L < 1 || D < 1) return 0;
   const size_t nsplit = (size_t)((L + mt::kDecSplit - 1) / mt::kDecSplit);
-  return ((size_t)B * Hq * nsplit * (D + 2) * sizeof(float) + 255) / 256 * 256;
+  return ((size_t)B * Hq * nsplit * (D + 4) * sizeof(float) + 255) / 256 * 256;  // rows of mt::dec_row<D>()
 }
 
 namespace {
@@ -668,6 +668,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
       (rc = check_tensor("v_cache", v_cache, strides + 8)) || (rc = check_tensor("o", o, strides + 12)))
     return rc;
   if (!workspace) return fail(MT_E_NULL, "workspace is NULL");
+  if (reinterpret_cast<uintptr_t>(workspace) % 16) return fail(MT_E_STRIDE, "workspace must be 16-byte aligned");
   if (workspace_bytes < mt_gqa_attn_decode_workspace_size(B, Hq, L, D))
     return fail(MT_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
                 mt_gqa_attn_decode_workspace_size(B, Hq, L, D));
@@ -688,14 +689,22 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid_s((unsigned)(B * Hkv * p.nsplit));
   const dim3 grid_c((unsigned)(((int64_t)B * Hq * D + 255) / 256));
-#define MT_DECODE_LAUNCH(E, DD)                                                                 \
-  hipLaunchKernelGGL((mt::attn_decode_split_kernel<E, DD>), grid_s, dim3(256), 0, st, p);     \
+  // the split kernel is instantiated per group size R = Hq / Hkv (1..8)
+#define MT_DECODE_SPLIT(E, DD, RR) \
+  case RR: hipLaunchKernelGGL((mt::attn_decode_split_kernel<E, DD, RR>), grid_s, dim3(64), 0, st, p); break
+#define MT_DECODE_LAUNCH(E, DD)                                                                            \
+  switch (p.R) {                                                                                           \
+    MT_DECODE_SPLIT(E, DD, 1); MT_DECODE_SPLIT(E, DD, 2); MT_DECODE_SPLIT(E, DD, 3); MT_DECODE_SPLIT(E, DD, 4); \
+    MT_DECODE_SPLIT(E, DD, 5); MT_DECODE_SPLIT(E, DD, 6); MT_DECODE_SPLIT(E, DD, 7); MT_DECODE_SPLIT(E, DD, 8); \
+    default: break;                                                                                        \
+  }                                                                                                        \
   hipLaunchKernelGGL((mt::attn_decode_combine_kernel<E, DD>), grid_c, dim3(256), 0, st, p)
   if (dtype == MT_DTYPE_BF16) {
     if (D == 32) { MT_DECODE_LAUNCH(mt::BF16, 32); } else if (D == 64) { MT_DECODE_LAUNCH(mt::BF16, 64); } else { MT_DECODE_LAUNCH(mt::BF16, 128); }
   } else {
     if (D == 32) { MT_DECODE_LAUNCH(mt::FP16, 32); } else if (D == 64) { MT_DECODE_LAUNCH(mt::FP16, 64); } else { MT_DECODE_LAUNCH(mt::FP16, 128); }
   }
+#undef MT_DECODE_SPLIT
 #undef MT_DECODE_LAUNCH
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "decode launch failed: %s", hipGetErrorString(e));
