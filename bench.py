@@ -8,10 +8,12 @@
 * value: TFLOP/s with the reference's FLOP convention extended to fwd+bwd,
   14 * B * Hq * D * T(T+1)/2 (scripts/benchmark_triton_attention.py:179-190
   gives the forward 4 * B * Hq * D * T(T+1)/2; backward adds 2.5x).
-* roofline: the dominant kernel's algorithmic MFMA FLOPs per launch over its
-  average duration, from HIP events that the library attaches to that
-  kernel's own dispatches (mt_time_next_kernel) on the launch stream; traffic
-  is its HBM bytes per launch from the committed rocprofv3 counter summary.
+* roofline: the dominant kernel's (the one-launch backward's) algorithmic
+  MFMA FLOPs per launch over its average duration within the headline's own
+  timed windows, from HIP events that the library attaches to each of its
+  dispatches (mt_time_kernel_queue; the backward runs on the autograd
+  engine's thread) on the launch stream; traffic is its HBM bytes per launch
+  from the committed rocprofv3 counter summary.
 * cpu_baseline: the reference's CPU attention path (torch SDPA, fp32, forward
   + autograd backward, model.py:228-235) on the host cores over a bounded
   sample of the same workload.
@@ -57,6 +59,7 @@ PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4096 FLOP/clk x 2.
 METRIC = "causal GQA fwd+bwd TFLOP/s (% bf16 MFMA peak) at T=1k/4k; train tokens/sec"
 
 # (B, T, Hq, Hkv, D)
+C1 = (2, 256, 4, 2, 32)     # fp32, N(0, 1), no RoPE: the reference's CPU-plumbing config
 C2 = (16, 1024, 8, 2, 64)
 C3 = (4, 4096, 16, 4, 64)
 C4 = (8, 2048, 32, 8, 128)
@@ -108,7 +111,7 @@ MIN_WARMUP = 25       # warm-up steps before the timed windows (the reference ha
 PREHEAT_S = 0.5       # and at least this long of back-to-back steps
 
 
-def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s=PREHEAT_S):
+def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s=PREHEAT_S, kernel_events=False):
     """fwd+bwd steps through the public op, timed in steady state.
 
     `warmup` untimed steps, then one timed window of `steps` steps (the cold
@@ -117,7 +120,11 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s
     run, then `repeats` timed windows of exactly `steps` steps each, every
     window bracketed by synchronisation and HIP events on the current stream.
     Returns ms per step: median, fastest and slowest window, the cold
-    window, and the median window's wall-clock time per step."""
+    window, and the median window's wall-clock time per step.  kernel_events:
+    also the average duration of the step's two main kernels (the forward and
+    the backward launch) over those windows, from HIP events the library
+    attaches to each of their dispatches (mt_time_kernel_queue: the backward
+    is launched from the autograd engine's thread)."""
     b, t, hq, hkv, d = cfg
     dev = torch.device("cuda:0")
     q, k, v, do = make_inputs(cfg, dev)
@@ -153,10 +160,28 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s
             step()
         n += 8
         torch.cuda.synchronize()
+    ev = None
+    if kernel_events:
+        lib = pkg._native.load()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(2 * steps * repeats)]
+        for a, b_ in ev:  # materialise the events on this device
+            a.record()
+            b_.record()
+        torch.cuda.synchronize()
+        arr = ctypes.c_void_p * len(ev)
+        pkg._native.check(lib.mt_time_kernel_queue(arr(*[a.cuda_event for a, _ in ev]),
+                                                   arr(*[b_.cuda_event for _, b_ in ev]), len(ev)),
+                          "mt_time_kernel_queue")
     runs = sorted(window() for _ in range(repeats))
     med_ms, med_wall = runs[len(runs) // 2]
-    return {"ms": med_ms, "ms_min": runs[0][0], "ms_max": runs[-1][0], "ms_cold": cold, "wall_ms": med_wall,
-            "repeats": repeats, "warmup_steps": n}
+    res = {"ms": med_ms, "ms_min": runs[0][0], "ms_max": runs[-1][0], "ms_cold": cold, "wall_ms": med_wall,
+           "repeats": repeats, "warmup_steps": n}
+    if ev is not None:
+        pkg._native.check(lib.mt_time_kernel_queue(None, None, 0), "mt_time_kernel_queue")
+        res["fwd_kernel_ms"] = sum(a.elapsed_time(b_) for a, b_ in ev[0::2]) / (len(ev) // 2)
+        res["bwd_kernel_ms"] = sum(a.elapsed_time(b_) for a, b_ in ev[1::2]) / (len(ev) // 2)
+    return res
 
 
 # The reference's own configs use other query-heads-per-KV-head ratios R:
@@ -365,25 +390,34 @@ def time_decode(pkg, lengths=(544, 1024), iters=50):
     return res
 
 
-def time_kernels(pkg, cfg, iters):
+def time_kernels(pkg, cfg, iters, fp32=False):
     """Average duration of each main kernel (HIP events the library records
     around it on its launch stream, one pair per launch) and of each whole
     stage: the forward stage adds the K-RoPE pass, the backward stage the
     delta prep pass (and the partial-sum combine pass when the dK/dV heads
     are split).  The backward kernel is also timed with only its dQ tasks
     and only its dK/dV tasks (the library's two half-backward entry points),
-    as a diagnostic of how the two kinds share the launch."""
+    as a diagnostic of how the two kinds share the launch.  fp32: BASELINE
+    config 1's form -- fp32 N(0, 1) inputs without RoPE, on the fp32 kernels."""
     native = pkg._native
     lib = native.load()
     b, t, hq, hkv, d = cfg
     dev = torch.device("cuda:0")
-    q, k, v, do = make_inputs(cfg, dev)
-    cos, sin = rope_tables(t, d, 10_000.0, dev)
+    if fp32:
+        g = torch.Generator().manual_seed(0)
+        q, k, v, do = (torch.randn(*shape, generator=g).to(dev)
+                       for shape in ((b, hq, t, d), (b, hkv, t, d), (b, hkv, t, d), (b, hq, t, d)))
+        cos = sin = None
+    else:
+        q, k, v, do = make_inputs(cfg, dev)
+        cos, sin = rope_tables(t, d, 10_000.0, dev)
+    dtype_code = native.DTYPE_FP32 if fp32 else native.DTYPE_BF16
+    ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
     o = torch.empty_like(q)
     lse = torch.empty((b, hq, t), device=dev, dtype=torch.float32)
     q_rot, k_rot = torch.empty_like(q), torch.empty_like(k)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws_bytes = lib.mt_gqa_attn_bwd_workspace_size(b, hq, hkv, t, d)
+    ws_bytes = lib.mt_gqa_attn_bwd_workspace_size_dtype(b, hq, hkv, t, d, dtype_code)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     s_fwd = native.strides_array(q, k, v, o)
     s_bwd = native.strides_array(q_rot, k_rot, v, o, do, dq, dk, dv)
@@ -391,15 +425,18 @@ def time_kernels(pkg, cfg, iters):
     sp = stream.cuda_stream
     scale = 1.0 / math.sqrt(d)
 
+    # with RoPE the backward takes the forward's rotated Q and K
+    qb, kb = (q, k) if cos is None else (q_rot, k_rot)
+
     def fwd():
         native.check(lib.mt_gqa_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
                                          q_rot.data_ptr(), k_rot.data_ptr(),
-                                         b, hq, hkv, t, d, s_fwd, scale, 0, cos.data_ptr(), sin.data_ptr(), sp), "fwd")
+                                         b, hq, hkv, t, d, s_fwd, scale, dtype_code, ptr(cos), ptr(sin), sp), "fwd")
 
     def bwd(fn):
-        native.check(fn(q_rot.data_ptr(), k_rot.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(),
+        native.check(fn(qb.data_ptr(), kb.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(),
                         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes,
-                        b, hq, hkv, t, d, s_bwd, scale, 0, cos.data_ptr(), sin.data_ptr(), sp), "bwd")
+                        b, hq, hkv, t, d, s_bwd, scale, dtype_code, ptr(cos), ptr(sin), sp), "bwd")
 
     stages = [("attn_fwd_kernel", fwd), ("attn_bwd_kernel", lambda: bwd(lib.mt_gqa_attn_bwd)),
               ("attn_bwd_kernel[dq]", lambda: bwd(lib.mt_gqa_attn_bwd_dq)),
@@ -768,7 +805,7 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="profiling driver: run only the decode step's attention kernels at the config 5 generation "
                          "shape, then a 256 MiB device copy (counter calibration), and print their timings")
-    ap.add_argument("--config", choices=("C2", "C3", "C4"), default="C3",
+    ap.add_argument("--config", choices=("C1", "C2", "C3", "C4"), default="C3",
                     help="BASELINE config that --kernels-only runs")
     args = ap.parse_args(argv)
     if args.gpus != 1:
@@ -793,21 +830,26 @@ def main(argv=None) -> int:
         return 0
 
     if args.kernels_only:
-        kern = time_kernels(pkg, {"C2": C2, "C3": C3, "C4": C4}[args.config], args.steps)
+        cfgs = {"C1": C1, "C2": C2, "C3": C3, "C4": C4}
+        kern = time_kernels(pkg, cfgs[args.config], args.steps, fp32=args.config == "C1")
         _calibration_copy()
         print(json.dumps({"kernels": kern, "copy_bytes_each_way": 256 << 20}), flush=True)
         return 0
 
     b, t, hq, hkv, d = C3
-    head = time_op_steps(pkg, C3, args.steps, args.warmup, rope=True)
+    head = time_op_steps(pkg, C3, args.steps, args.warmup, rope=True, kernel_events=True)
     ms_event = head["ms"]
     flops = fwd_bwd_flops(b, t, hq, d)
     value = flops / (ms_event * 1e-3) / 1e12
     tflops = lambda ms: round(flops / (ms * 1e-3) / 1e12, 2)  # noqa: E731
 
+    # the dominant kernel: the one-launch backward; its duration is averaged
+    # over the headline's own timed windows (events on each of its dispatches)
     kern = time_kernels(pkg, C3, max(10, args.steps // 2))
-    dom = max((n for n in kern if "[" not in n), key=lambda n: kern[n]["ms"])
-    achieved = kern[dom]["tflops"]
+    dom = "attn_bwd_kernel"
+    unit_flop = b * hq * d * pairs(t)
+    dom_ms = head["bwd_kernel_ms"]
+    achieved = KERNEL_FLOP_UNITS[dom][0] * unit_flop / (dom_ms * 1e-3) / 1e12
 
     ms_c2 = time_op_steps(pkg, C2, args.steps, args.warmup, rope=True)["ms"]
     group_sizes = time_group_sizes(pkg, args.steps)
@@ -832,6 +874,8 @@ def main(argv=None) -> int:
             "ms_median": round(head["ms"], 4), "ms_fastest": round(head["ms_min"], 4),
             "ms_slowest": round(head["ms_max"], 4), "tflops_slowest": tflops(head["ms_max"]),
             "ms_cold_window": round(head["ms_cold"], 4), "tflops_cold_window": tflops(head["ms_cold"]),
+            "fwd_kernel_ms_in_windows": round(head["fwd_kernel_ms"], 4),
+            "bwd_kernel_ms_in_windows": round(head["bwd_kernel_ms"], 4),
         },
         "higher_is_better": True,
         "scaling": "weak",
@@ -850,6 +894,8 @@ def main(argv=None) -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "kernel_ms": round(dom_ms, 4),
+            "executed_tflops": round(KERNEL_FLOP_UNITS[dom][1] * unit_flop / (dom_ms * 1e-3) / 1e12, 2),
             "traffic": hbm_traffic(dom),
         },
         "kernels": {n: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 1),

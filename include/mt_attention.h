@@ -174,6 +174,16 @@ int mt_gqa_attn_bwd_dkv(const void* q, const void* k, const void* v, const void*
 int mt_time_next_kernel(void* start_event, void* stop_event);
 
 /*
+ * As mt_time_next_kernel for the next n main kernels launched by any thread
+ * of the process, in launch order: launch i takes start_events[i] and
+ * stop_events[i].  A thread's own mt_time_next_kernel arming is used first.
+ * For timing kernels that a framework launches from its own threads (the
+ * backward runs on the autograd engine's device thread).  The arrays are
+ * copied; n = 0 disarms.  No reference counterpart (benchmark support).
+ */
+int mt_time_kernel_queue(void* const* start_events, void* const* stop_events, int n);
+
+/*
  * Decode attention for KV-cached generation: one new query token per sequence
  * (at position L-1) against cached keys/values 0..L-1.  It replaces the
  * attention inside the per-token full recompute of TradingModel.generate,

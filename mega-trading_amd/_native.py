@@ -33,6 +33,7 @@ EXPORTS = (
     "mt_gqa_attn_bwd_dkv",
     "mt_gqa_attn_bwd_noalloc",
     "mt_time_next_kernel",
+    "mt_time_kernel_queue",
     "mt_rms_norm_fwd",
     "mt_add_rms_norm_fwd",
     "mt_rms_norm_bwd_workspace_size",
@@ -65,6 +66,7 @@ _BWD_ARGTYPES = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _I, _I, _I, _I, _I,
 _L = ctypes.c_int64
 _OPS_SIGNATURES = {
     "mt_gqa_attn_bwd_workspace_size_dtype": (_S, [_I, _I, _I, _I, _I, _I]),
+    "mt_time_kernel_queue": (_I, [_P, _P, _I]),
     "mt_gqa_attn_bwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P, _P, _P]),
     "mt_rms_norm_fwd": (_I, [_P, _L, _P, _P, _P, _L, _I, _F, _I, _I, _P]),
     "mt_add_rms_norm_fwd": (_I, [_P, _L, _P, _L, _P, _P, _P, _P, _L, _I, _F, _I, _I, _P]),

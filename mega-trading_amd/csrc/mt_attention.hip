@@ -13,6 +13,8 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include "../../include/mt_attention.h"
 #include "attn_f32_kernels.h"
@@ -68,10 +70,25 @@ using mt_abi::ok;
 thread_local hipEvent_t g_time_start = nullptr;
 thread_local hipEvent_t g_time_stop = nullptr;
 
+// Process-wide queue armed by mt_time_kernel_queue(): event pairs taken in
+// launch order by main kernel launches of any thread (after this thread's own
+// mt_time_next_kernel arming).
+std::mutex g_time_mu;
+std::vector<std::pair<hipEvent_t, hipEvent_t>> g_time_queue;
+size_t g_time_next = 0;
+
 template <class K>
 hipError_t launch_main(K kernel, dim3 grid, dim3 block, hipStream_t st, const mt::AttnParams& p) {
   hipEvent_t a = g_time_start, b = g_time_stop;
   g_time_start = g_time_stop = nullptr;
+  if (!a) {
+    std::lock_guard<std::mutex> lock(g_time_mu);
+    if (g_time_next < g_time_queue.size()) {
+      a = g_time_queue[g_time_next].first;
+      b = g_time_queue[g_time_next].second;
+      ++g_time_next;
+    }
+  }
   hipExtLaunchKernelGGL(kernel, grid, block, 0, st, a, b, 0, p);
   return hipGetLastError();
 }
@@ -547,6 +564,19 @@ extern "C" {
 int mt_version(void) { return (0 << 16) | 5; }
 
 const char* mt_last_error(void) { return mt_abi::last_error(); }
+
+int mt_time_kernel_queue(void* const* start_events, void* const* stop_events, int n) {
+  if (n < 0) return fail(MT_E_SHAPE, "n must be >= 0 (got %d)", n);
+  if (n > 0 && (!start_events || !stop_events)) return fail(MT_E_NULL, "event arrays are NULL");
+  for (int i = 0; i < n; ++i)
+    if (!start_events[i] || !stop_events[i]) return fail(MT_E_NULL, "event pair %d has a NULL event", i);
+  std::lock_guard<std::mutex> lock(g_time_mu);
+  g_time_queue.clear();
+  for (int i = 0; i < n; ++i)
+    g_time_queue.emplace_back(static_cast<hipEvent_t>(start_events[i]), static_cast<hipEvent_t>(stop_events[i]));
+  g_time_next = 0;
+  return ok();
+}
 
 int mt_time_next_kernel(void* start_event, void* stop_event) {
   if ((start_event == nullptr) != (stop_event == nullptr))

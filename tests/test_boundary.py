@@ -151,6 +151,12 @@ def test_kernel_timer_arming(mta):
     assert b"both" in lib.mt_last_error()
     assert lib.mt_time_next_kernel(None, None) == 0  # disarm
     assert lib.mt_last_error() == b""
+    # the process-wide queue: argument checks (no events are created here)
+    arr = (ctypes.c_void_p * 2)(0x1000, None)
+    assert lib.mt_time_kernel_queue(None, None, -1) == -2
+    assert lib.mt_time_kernel_queue(None, None, 2) == -1
+    assert lib.mt_time_kernel_queue(arr, arr, 2) == -1  # a NULL event in a pair
+    assert lib.mt_time_kernel_queue(None, None, 0) == 0  # disarm
 
 
 def test_c_abi_rejects_bad_arguments_before_launch(mta):
