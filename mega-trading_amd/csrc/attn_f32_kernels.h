@@ -80,16 +80,20 @@ template <int D, bool ROPE>
 __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnParams p) {
   constexpr int HD = D / 2;  // d values per lane
   constexpr int DT = D / 32;
+  __shared__ f32x4 red_o[3][DT * 4][64];  // waves 1-3: [wave - 1][dt, g][lane] unnormalised O
+  __shared__ f32x2 red_ml[3][64];         // and (m, l)
   const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = threadIdx.x >> 6;
   const int nblk = (p.T + 31) / 32;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= p.B * p.Hq * nblk) return;
+  const int t = blockIdx.x;
+  if (t >= p.B * p.Hq * nblk) return;  // (workgroup-uniform)
   const F32Task task = f32_task(t, p.B, p.Hq, nblk, true);
   const int kvh = task.h / p.R;
   const int row = task.blk * 32 + l32;
   const int rc = min(row, p.T - 1);
 
-  // the lane's half of its query row, rotated if RoPE (and written to q_rot)
+  // the lane's half of its query row, rotated if RoPE (and written to q_rot,
+  // by wave 0)
   float qv[HD];
   {
     const float* qr = fptr(p.q) + task.b * p.sq[0] + (int64_t)task.h * p.sq[1] + (int64_t)rc * p.sq[2] + hh * HD;
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnParams p) {
         const f32x2 sn = *reinterpret_cast<const f32x2*>(p.sin + (int64_t)rc * (D / 2) + d0 / 2);
         x = f32x4{x[0] * cs[0] - x[1] * sn[0], x[0] * sn[0] + x[1] * cs[0], x[2] * cs[1] - x[3] * sn[1],
                   x[2] * sn[1] + x[3] * cs[1]};
-        if (row < p.T)
+        if (wave == 0 && row < p.T)
           *reinterpret_cast<f32x4*>(fptr(p.qrot) + (((int64_t)task.b * p.Hq + task.h) * p.T + row) * D + d0) = x;
       }
 #pragma unroll
@@ -117,7 +121,9 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnParams p) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) zero16(oacc[dt]);
   float m = -INFINITY, l = 0.f;
-  for (int kt = 0; kt <= task.blk; ++kt) {
+  // the key tiles on or left of the diagonal are dealt to the 4 waves in turn;
+  // each keeps its own running offset and sums, merged below
+  for (int kt = wave; kt <= task.blk; kt += 4) {
     // S^T (lane = query, slots = keys)
     const float* kr = kbase + (int64_t)min(kt * 32 + l32, p.T - 1) * p.sk[2] + hh * HD;
     f32x16 s = {};
@@ -134,7 +140,8 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnParams p) {
       s[i] = (key <= row && key < p.T) ? s[i] * c2 : -INFINITY;
       mx = fmaxf(mx, s[i]);
     }
-    // every row sees key 0 in its first tile, so m is finite from then on
+    // every tile left of the diagonal is unmasked and the diagonal tile holds
+    // key 32 kt <= row, so m is finite after a wave's first tile
     const float mnew = fmaxf(m, max_with_partner(mx));
     const float alpha = exp2_fast(m - mnew);
     float ps = 0.f;
@@ -156,6 +163,49 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnParams p) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) oacc[dt] = mfma_f32(vr[32 * dt], s[j], oacc[dt]);
     }
+  }
+  // merge the four waves' (O, m, l) with the log-sum-exp rule (a wave that
+  // had no tile has m = -inf and contributes nothing); m is the same on a
+  // lane and its lane^32 partner
+  if (wave > 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        red_o[wave - 1][dt * 4 + g][lane] =
+            f32x4{oacc[dt][4 * g], oacc[dt][4 * g + 1], oacc[dt][4 * g + 2], oacc[dt][4 * g + 3]};
+    red_ml[wave - 1][lane] = f32x2{m, l};
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  {
+    f32x2 ml[3];
+    float mm = m;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      ml[w] = red_ml[w][lane];
+      mm = fmaxf(mm, ml[w][0]);
+    }
+    const float a0 = exp2_fast(m - mm);
+    l *= a0;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[dt][i] *= a0;
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      const float aw = exp2_fast(ml[w][0] - mm);
+      l = __builtin_fmaf(aw, ml[w][1], l);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 o = red_o[w][dt * 4 + g][lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) oacc[dt][4 * g + e] = __builtin_fmaf(aw, o[e], oacc[dt][4 * g + e]);
+        }
+    }
+    m = mm;
   }
   if (row >= p.T) return;
   const float lt = sum_with_partner(l);
@@ -199,17 +249,21 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_f32_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward dQ: per 32-key tile S^T and dP^T recomputed (lane = query),
-// P = 2^(S c - LSE2), dS = P (dP - delta), dQ^T += K^T dS^T.
+// Backward dQ: per workgroup 32 query rows of one head; the 32-key tiles on
+// or left of the diagonal are dealt to the 4 waves in turn (each recomputes
+// S^T and dP^T for its tiles, lane = query: P = 2^(S c - LSE2), dS = P (dP -
+// delta), dQ^T += K^T dS^T), and the four partial sums are added through LDS.
 // ---------------------------------------------------------------------------
 template <int D, bool ROPE>
 __global__ __launch_bounds__(256) void attn_bwd_dq_f32_kernel(AttnParams p) {
   constexpr int HD = D / 2;
   constexpr int DT = D / 32;
+  __shared__ f32x4 red[3][DT * 4][64];  // waves 1-3: [wave - 1][dt, g][lane]
   const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = threadIdx.x >> 6;
   const int nblk = (p.T + 31) / 32;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= p.B * p.Hq * nblk) return;
+  const int t = blockIdx.x;
+  if (t >= p.B * p.Hq * nblk) return;  // (workgroup-uniform)
   const F32Task task = f32_task(t, p.B, p.Hq, nblk, true);
   const int kvh = task.h / p.R;
   const int row = task.blk * 32 + l32;
@@ -240,7 +294,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_f32_kernel(AttnParams p) {
   f32x16 dq[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) zero16(dq[dt]);
-  for (int kt = 0; kt <= task.blk; ++kt) {
+  for (int kt = wave; kt <= task.blk; kt += 4) {
     const int kc = min(kt * 32 + l32, p.T - 1);
     const float* kr = kbase + (int64_t)kc * p.sk[2] + hh * HD;
     const float* vr = vbase + (int64_t)kc * p.sv[2] + hh * HD;
@@ -268,6 +322,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_f32_kernel(AttnParams p) {
       for (int dt = 0; dt < DT; ++dt) dq[dt] = mfma_f32(kj[32 * dt], s[j], dq[dt]);
     }
   }
+  // the four waves' partial sums: waves 1-3 hand theirs to wave 0
+  if (wave > 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        red[wave - 1][dt * 4 + g][lane] = f32x4{dq[dt][4 * g], dq[dt][4 * g + 1], dq[dt][4 * g + 2], dq[dt][4 * g + 3]};
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 a = red[w][dt * 4 + g][lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dq[dt][4 * g + e] += a[e];
+      }
   if (row >= p.T) return;
   float* out = fptr(p.out) + task.b * p.sout[0] + (int64_t)task.h * p.sout[1] + (int64_t)row * p.sout[2];
 #pragma unroll
@@ -284,18 +358,24 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_f32_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward dK / dV: per wave 32 keys of one KV head, K and V in registers;
-// over the group's heads and the 32-row tiles on or below the diagonal:
-// S and dP recomputed (lane = key, slots = rows), dV^T += dO^T P, dK^T += Q^T dS.
+// Backward dK / dV: per workgroup 32 keys of one KV head, K and V in
+// registers; the (query head, 32-row tile on or below the diagonal) pairs of
+// the block are dealt to the 4 waves in turn (each recomputes S and dP for its
+// pairs: lane = key, slots = rows; dV^T += dO^T P, dK^T += Q^T dS), and the
+// four partial sums are added through LDS.  A wave per key block would leave
+// most of the GPU idle at small shapes (32 waves on 1024
+// SIMDs, the longest walking every row of its heads).
 // ---------------------------------------------------------------------------
 template <int D, bool ROPE>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_f32_kernel(AttnParams p) {
   constexpr int HD = D / 2;
   constexpr int DT = D / 32;
+  __shared__ f32x4 red[3][2 * DT * 4][64];  // waves 1-3: [wave - 1][dK / dV, dt, g][lane]
   const int lane = threadIdx.x & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = threadIdx.x >> 6;
   const int nblk = (p.T + 31) / 32;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= p.B * p.Hkv * nblk) return;
+  const int t = blockIdx.x;
+  if (t >= p.B * p.Hkv * nblk) return;  // (workgroup-uniform)
   const F32Task task = f32_task(t, p.B, p.Hkv, nblk, false);  // smallest key block (most rows) first
   const int key = task.blk * 32 + l32;
   const int kc = min(key, p.T - 1);
@@ -322,12 +402,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_f32_kernel(AttnParams p) {
     zero16(dk[dt]);
     zero16(dv[dt]);
   }
-  for (int r = 0; r < p.R; ++r) {
+  const int ntile = nblk - task.blk;  // row tiles per head on or below the diagonal
+  for (int u = wave; u < p.R * ntile; u += 4) {
+    const int r = u % p.R;
+    const int qt = task.blk + u / p.R;
     const int head = task.h * p.R + r;
     const float* qbase = fptr(p.q) + task.b * p.sq[0] + (int64_t)head * p.sq[1];
     const float* gbase = fptr(p.dout) + task.b * p.sdo[0] + (int64_t)head * p.sdo[1];
     const int64_t rowbase = ((int64_t)task.b * p.Hq + head) * p.T;
-    for (int qt = task.blk; qt < nblk; ++qt) {
+    {
       // S and dP: rows m = the tile's queries, lane = key
       const int qa = min(qt * 32 + l32, p.T - 1);
       const float* qr = qbase + (int64_t)qa * p.sq[2] + hh * HD;
@@ -365,6 +448,32 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_f32_kernel(AttnParams p) {
       }
     }
   }
+  // the four waves' partial sums: waves 1-3 hand theirs to wave 0
+  if (wave > 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        red[wave - 1][dt * 4 + g][lane] = f32x4{dk[dt][4 * g], dk[dt][4 * g + 1], dk[dt][4 * g + 2], dk[dt][4 * g + 3]};
+        red[wave - 1][(DT + dt) * 4 + g][lane] =
+            f32x4{dv[dt][4 * g], dv[dt][4 * g + 1], dv[dt][4 * g + 2], dv[dt][4 * g + 3]};
+      }
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 a = red[w][dt * 4 + g][lane], b = red[w][(DT + dt) * 4 + g][lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dk[dt][4 * g + e] += a[e];
+          dv[dt][4 * g + e] += b[e];
+        }
+      }
   if (key >= p.T) return;
   float* dkr = fptr(p.dk) + task.b * p.sdk[0] + (int64_t)task.h * p.sdk[1] + (int64_t)key * p.sdk[2];
   float* dvr = fptr(p.dv) + task.b * p.sdv[0] + (int64_t)task.h * p.sdv[1] + (int64_t)key * p.sdv[2];

@@ -410,8 +410,8 @@ hipError_t launch_fwd_f32(mt::AttnParams p, hipStream_t st, int) {
     p.sk[1] = (int64_t)p.T * D;
     p.sk[2] = D;
   }
-  const int64_t waves = (int64_t)p.B * p.Hq * ((p.T + 31) / 32);
-  return launch_main(mt::attn_fwd_f32_kernel<D, ROPE>, dim3((unsigned)((waves + 3) / 4)), dim3(256), st, p);
+  const int64_t blocks = (int64_t)p.B * p.Hq * ((p.T + 31) / 32);  // one 4-wave workgroup per (batch, head, 32 rows)
+  return launch_main(mt::attn_fwd_f32_kernel<D, ROPE>, dim3((unsigned)blocks), dim3(256), st, p);
 }
 
 template <int D, bool ROPE>
@@ -424,13 +424,13 @@ hipError_t launch_bwd_f32(mt::AttnParams p, hipStream_t st, int stage) {
                        dim3(256), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t waves = (int64_t)p.B * p.Hq * nblk;
-    e = launch_main(mt::attn_bwd_dq_f32_kernel<D, ROPE>, dim3((unsigned)((waves + 3) / 4)), dim3(256), st, p);
+    const int64_t blocks = (int64_t)p.B * p.Hq * nblk;  // one 4-wave workgroup per (batch, head, 32 rows)
+    e = launch_main(mt::attn_bwd_dq_f32_kernel<D, ROPE>, dim3((unsigned)blocks), dim3(256), st, p);
     if (e != hipSuccess) return e;
   }
   if (stage & 2) {
-    const int64_t waves = (int64_t)p.B * p.Hkv * nblk;
-    hipError_t e = launch_main(mt::attn_bwd_dkv_f32_kernel<D, ROPE>, dim3((unsigned)((waves + 3) / 4)), dim3(256), st, p);
+    const int64_t blocks = (int64_t)p.B * p.Hkv * nblk;  // one 4-wave workgroup per (batch, KV head, 32 keys)
+    hipError_t e = launch_main(mt::attn_bwd_dkv_f32_kernel<D, ROPE>, dim3((unsigned)blocks), dim3(256), st, p);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
