@@ -322,13 +322,15 @@ def time_decode(pkg, lengths=(544, 1024), iters=50):
     """One decode step's attention kernels at the config 5 generation shape
     (32 rollouts, Hq 8, Hkv 2, D 64, a 1024-position bf16 cache), through the
     C ABI with preallocated buffers, the length read from device memory as the
-    recorded decode step does: the split + combine pair (mt_gqa_attn_decode_dev)
-    and the RoPE / cache-append kernel, each timed over `iters` back-to-back
-    launches with HIP events.  Algorithmic bytes: the split kernel reads the
-    group's q and L cached K and V rows once and writes one fp32 partial
-    (o, m, l) per 64-key split; the combine reads the partials and writes O;
-    the append reads the fp32 q / k / v projections and writes q_rot and one
-    K and one V cache row."""
+    recorded decode step does: the attention (mt_gqa_attn_decode_dev; at this
+    capacity the split + combine pair) and the RoPE / cache-append kernel,
+    each timed over `iters` back-to-back launches with HIP events.
+    Algorithmic bytes: the attention reads the group's q and L cached K and V
+    rows once and writes O; the split + combine pair also writes and reads
+    one fp32 partial (o, m, l) per head and 64-key split (the fused one-launch
+    kernel, used for caches of at most 512 keys, has none); the append reads
+    the fp32 q / k / v projections and writes q_rot and one K and one V cache
+    row."""
     native = pkg._native
     lib = native.load()
     dev = torch.device("cuda:0")
@@ -352,6 +354,8 @@ def time_decode(pkg, lengths=(544, 1024), iters=50):
     ins = (ctypes.c_int64 * 6)(xq.stride(0), xq.stride(1), xk.stride(0), xk.stride(1), xv.stride(0), xv.stride(1))
     cst = (ctypes.c_int64 * 6)(*kc.stride()[:3], *vc.stride()[:3])
     scale = 1.0 / math.sqrt(d)
+    # the library decodes a cache of at most 8 splits of 64 keys in one fused launch
+    fused = (cap + 63) // 64 <= 8
     res = {}
 
     def timed(fn, n):
@@ -377,15 +381,18 @@ def time_decode(pkg, lengths=(544, 1024), iters=50):
             q_rot.data_ptr(), kc.data_ptr(), vc.data_ptr(), cst, cap, b, hq, hkv, d, native.DTYPE_FP32,
             native.DTYPE_BF16, sp), "mt_decode_rope_append")
         kv_bytes = 2 * b * hkv * L * d * 2
-        part_bytes = b * hq * ns * (d + 2) * 4
-        split_bytes = kv_bytes + b * hq * d * 2 + part_bytes
-        comb_bytes = part_bytes + b * hq * d * 2
+        qo_bytes = 2 * b * hq * d * 2
+        if fused:  # K, V rows 0..L-1, q and out; no partials
+            attn_bytes = kv_bytes + qo_bytes
+        else:  # plus one fp32 partial per head and split, written once and read once
+            attn_bytes = kv_bytes + qo_bytes + 2 * b * hq * ns * (d + 2) * 4
         us = timed(attn, iters)
         us_app = timed(append, iters)
         app_bytes = b * (hq + 2 * hkv) * d * 4 + b * (hq + 2 * hkv) * d * 2 + d * 4
-        res[f"L{L}"] = {"attention_us": round(us, 2), "split_bytes": split_bytes, "combine_bytes": comb_bytes,
-                        "attention_GBps": round((split_bytes + comb_bytes) / (us * 1e-6) / 1e9, 1),
+        res[f"L{L}"] = {"attention_us": round(us, 2), "attention_bytes": attn_bytes,
+                        "attention_GBps": round(attn_bytes / (us * 1e-6) / 1e9, 1),
                         "rope_append_us": round(us_app, 2), "rope_append_bytes": app_bytes}
+    res["attention_kernels"] = "attn_decode_fused_kernel" if fused else "attn_decode_split_kernel + attn_decode_combine_kernel"
     res["shape"] = "B=32 Hq=8 Hkv=2 D=64 bf16 cache of 1024 positions, length from device memory"
     return res
 

@@ -9,13 +9,16 @@
 // wave scores its split for all R query heads of the KV group (each K/V row is
 // read once for the R heads), forms the split's softmax numerator and offset,
 // and writes an fp32 partial (o, m, l).  A second kernel merges the splits
-// with the log-sum-exp rule.  The work is HBM- and latency-bound (the cache is
-// read once; at the decoder's shapes a split's data is a few KB), so it uses
-// plain fp32 FMAs -- with one query row per head there is no matrix product to
-// feed the MFMAs -- and is laid out for few dependent steps: every K and V
-// load of a lane is issued at entry, the reductions stay inside the wave (DPP
-// within 16-lane rows, permlane swaps across rows), and one LDS exchange hands
-// the probabilities from the score layout (lane = key) to the V layout.
+// with the log-sum-exp rule; a cache of at most 8 splits is decoded in one
+// launch instead (one workgroup per (batch, KV head), its waves merged in
+// LDS).  The work is HBM- and latency-bound (the cache is read once; at the
+// decoder's shapes a split's data is a few KB), so it runs on the vector ALUs
+// -- with one query row per head there is no matrix product to feed the
+// MFMAs: q . k as v_dot2 on the stored 16-bit pairs, p V as fp32 FMAs -- and
+// is laid out for few dependent steps: every K and V load of a lane is issued
+// at entry, the reductions stay inside the wave (DPP within 16-lane rows,
+// permlane swaps across rows), and one LDS exchange hands the probabilities
+// from the score layout (lane = key) to the V layout.
 #pragma once
 
 #include "mt_common.h"
@@ -74,85 +77,81 @@ __device__ __forceinline__ float wave_reduce(float x) {
   return red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// R (query heads of the KV group) is a template parameter: the per-head loops
-// then unroll into straight-line code whose LDS reads issue back to back (with
-// a run-time R every head is a branch with its own wait on its reads).
-template <class E, int D, int R>
-__global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeParams p) {
-  static_assert(D == 32 || D == 64 || D == 128, "head size");
-  static_assert(R >= 1 && R <= kDecMaxR, "group size");
-  constexpr int NC = D / 8;                 // 16-byte chunks per row
-  constexpr int G = 64 / NC;                // key groups of the V pass
-  constexpr int NV = kDecSplit / G;         // V chunks per lane
-  constexpr int LO = NC == 4 ? 2 : NC == 8 ? 3 : 4;  // log2(NC): lane bits of the d chunk
-  __shared__ f32x4 qs[R][D / 4];
-  __shared__ float ps[R][kDecSplit];
-  const int lane = threadIdx.x;
-  const int s = blockIdx.x % p.nsplit;
-  const int g = blockIdx.x / p.nsplit;
-  const int kvh = g % p.Hkv;
-  const int b = g / p.Hkv;
-  const int k0 = s * kDecSplit;
-  const int L = decode_length(p);
-  if (k0 >= L) return;  // a split past the current length (device-length launches cover the capacity)
-  const int n = min(kDecSplit, L - k0);
-
-  // Every K and V load first (one memory round trip).  Score layout: lane =
-  // key k0 + lane.  V layout: lane = (d chunk c = lane % NC, key group
-  // lane / NC), keys j = lane / NC + i G.  Keys past the split's end load its
-  // last key instead (in bounds; their probabilities are zero).
-  const int c = lane % NC;
-  const int kg = lane / NC;
-  u32x4 kw[NC], vw[NV];
-  {
-    const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + min(lane, n - 1)) * p.sk[2];
-#pragma unroll
-    for (int cc = 0; cc < NC; ++cc) kw[cc] = *reinterpret_cast<const u32x4*>(krow + 8 * cc);
-    const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2] + 8 * c;
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      vw[i] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)min(kg + i * G, n - 1) * p.sv[2]);
-  }
-  // the group's R query rows, as fp32 in LDS (read back as broadcasts)
-  {
-    const uint16_t* qb = p.q + b * p.sq[0] + (int64_t)(kvh * R) * p.sq[1];
-#pragma unroll
-    for (int i0 = 0; i0 < R * NC; i0 += 64) {
-      const int i = i0 + lane;
-      if (i < R * NC) {
-        const int h = i / NC, cc = i % NC;
-        const u32x4 w = *reinterpret_cast<const u32x4*>(qb + (int64_t)h * p.sq[1] + 8 * cc);
-        qs[h][2 * cc] = f32x4{lo_f<E>(w[0]), hi_f<E>(w[0]), lo_f<E>(w[1]), hi_f<E>(w[1])};
-        qs[h][2 * cc + 1] = f32x4{lo_f<E>(w[2]), hi_f<E>(w[2]), lo_f<E>(w[3]), hi_f<E>(w[3])};
-      }
-    }
-  }
-  __syncthreads();
-
-  // scores of key k0 + lane for every head (log2 units), the split's per-head
-  // offset m and probability sum l
-  float sc[R];
+// q . k of one cached row for each of the R heads: two products per
+// v_dot2c_f32 (exact 16-bit products, fp32 sums) straight from the stored
+// pairs, with no conversion of k.
+template <class E, int NC, int R>
+__device__ __forceinline__ void dec_scores(const u32x4 (&qs)[R][NC], const u32x4 (&kw)[NC], float (&sc)[R]) {
 #pragma unroll
   for (int h = 0; h < R; ++h) sc[h] = 0.f;
 #pragma unroll
-  for (int cc = 0; cc < NC; ++cc) {
-    float kv[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      kv[2 * e] = lo_f<E>(kw[cc][e]);
-      kv[2 * e + 1] = hi_f<E>(kw[cc][e]);
-    }
+  for (int cc = 0; cc < NC; ++cc)
 #pragma unroll
     for (int h = 0; h < R; ++h) {
-      const f32x4 q0 = qs[h][2 * cc], q1 = qs[h][2 * cc + 1];
+      const u32x4 qv = qs[h][cc];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sc[h] = __builtin_fmaf(q0[e], kv[e], sc[h]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sc[h] = __builtin_fmaf(q1[e], kv[4 + e], sc[h]);
+      for (int e = 0; e < 4; ++e) sc[h] = E::dot2(qv[e], kw[cc][e], sc[h]);
     }
+}
+
+// One 64-key split [k0, k0 + n) of one (batch, KV head), computed by one wave
+// for the R query heads of the group; shared by the split kernel (which writes
+// the result to HBM) and the fused kernel (which merges its waves in LDS).
+//
+// Layouts.  Score pass: lane = key k0 + lane.  V pass: lane = (d chunk
+// c = lane % NC, key group lane / NC), keys j = lane / NC + i G.  Keys past the
+// split's end load its last key instead (in bounds; their probabilities are
+// zero), so the loads need no branches.
+template <int D>
+struct DecLayout {
+  static constexpr int NC = D / 8;          // 16-byte chunks per row
+  static constexpr int G = 64 / NC;         // key groups of the V pass
+  static constexpr int NV = kDecSplit / G;  // V chunks per lane
+  static constexpr int LO = NC == 4 ? 2 : NC == 8 ? 3 : 4;  // log2(NC): lane bits of the d chunk
+};
+
+// Every K and V load of the split, issued together (one memory round trip).
+template <int D>
+__device__ __forceinline__ void dec_load(const DecodeParams& p, int b, int kvh, int k0, int n, int lane,
+                                         u32x4 (&kw)[DecLayout<D>::NC], u32x4 (&vw)[DecLayout<D>::NV]) {
+  using Ly = DecLayout<D>;
+  const int c = lane % Ly::NC, kg = lane / Ly::NC;
+  const uint16_t* krow = p.k + b * p.sk[0] + (int64_t)kvh * p.sk[1] + (int64_t)(k0 + min(lane, n - 1)) * p.sk[2];
+#pragma unroll
+  for (int cc = 0; cc < Ly::NC; ++cc) kw[cc] = *reinterpret_cast<const u32x4*>(krow + 8 * cc);
+  const uint16_t* vbase = p.v + b * p.sv[0] + (int64_t)kvh * p.sv[1] + (int64_t)k0 * p.sv[2] + 8 * c;
+#pragma unroll
+  for (int i = 0; i < Ly::NV; ++i)
+    vw[i] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)min(kg + i * Ly::G, n - 1) * p.sv[2]);
+}
+
+// The group's q rows, [R][NC] 16-byte chunks as stored, staged in LDS by the
+// workgroup's threads (read back as broadcasts).
+template <int D, int R>
+__device__ __forceinline__ void dec_stage_q(const DecodeParams& p, int b, int kvh, int tid, int nthreads,
+                                            u32x4 (&qs)[R][DecLayout<D>::NC]) {
+  constexpr int NC = DecLayout<D>::NC;
+  const uint16_t* qb = p.q + b * p.sq[0] + (int64_t)(kvh * R) * p.sq[1];
+  for (int i = tid; i < R * NC; i += nthreads) {
+    const int h = i / NC, cc = i % NC;
+    qs[h][cc] = *reinterpret_cast<const u32x4*>(qb + (int64_t)h * p.sq[1] + 8 * cc);
   }
+}
+
+// The split's softmax offset m and sum l per head (log2 units) and its
+// unnormalised o[h][8 c .. 8 c + 7] = sum_j p[h][j] V[k0 + j][...], summed
+// over the key groups (lanes with kg = 0 hold the result).  ps is the wave's
+// own [R][64] LDS block; one exchange through it moves the probabilities from
+// the score layout to the V layout.
+template <class E, int D, int R>
+__device__ __forceinline__ void dec_split(const DecodeParams& p, int n, int lane, const u32x4 (&qs)[R][DecLayout<D>::NC],
+                                          const u32x4 (&kw)[DecLayout<D>::NC], const u32x4 (&vw)[DecLayout<D>::NV],
+                                          float (&ps)[R][kDecSplit], float (&m)[R], float (&l)[R],
+                                          float (&acc)[R][8]) {
+  using Ly = DecLayout<D>;
+  float sc[R];
+  dec_scores<E, Ly::NC, R>(qs, kw, sc);
   const bool live = lane < n;
-  float m[R], l[R];
 #pragma unroll
   for (int h = 0; h < R; ++h) {
     const float x = live ? sc[h] * p.scale_log2 : -INFINITY;
@@ -161,18 +160,19 @@ __global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeParams p) {
     ps[h][lane] = e;
     l[h] = wave_reduce<0, false>(e);
   }
-  __syncthreads();
-
-  // o[h][d] = sum_j p[h][j] V[k0 + j][d]: lane (c, kg) sums its NV keys for the
-  // 8 d values of chunk c, then the G key groups are summed across lanes
-  float acc[R][8];
+  // LDS operations of one wave complete in order: a wave-scope fence (a
+  // compiler barrier) suffices between the writes and the reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int kg = lane / Ly::NC;
 #pragma unroll
   for (int h = 0; h < R; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int j = kg + i * G;
+  for (int i = 0; i < Ly::NV; ++i) {
+    const int j = kg + i * Ly::G;
     float vv[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -189,8 +189,36 @@ __global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeParams p) {
 #pragma unroll
   for (int h = 0; h < R; ++h)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = wave_reduce<LO, false>(acc[h][e]);
-  if (kg == 0) {
+    for (int e = 0; e < 8; ++e) acc[h][e] = wave_reduce<Ly::LO, false>(acc[h][e]);
+}
+
+// R (query heads of the KV group) is a template parameter: the per-head loops
+// then unroll into straight-line code whose LDS reads issue back to back (with
+// a run-time R every head is a branch with its own wait on its reads).
+template <class E, int D, int R>
+__global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeParams p) {
+  static_assert(D == 32 || D == 64 || D == 128, "head size");
+  static_assert(R >= 1 && R <= kDecMaxR, "group size");
+  using Ly = DecLayout<D>;
+  __shared__ u32x4 qs[R][Ly::NC];
+  __shared__ float ps[R][kDecSplit];
+  const int lane = threadIdx.x;
+  const int s = blockIdx.x % p.nsplit;
+  const int g = blockIdx.x / p.nsplit;
+  const int kvh = g % p.Hkv;
+  const int b = g / p.Hkv;
+  const int k0 = s * kDecSplit;
+  const int L = decode_length(p);
+  if (k0 >= L) return;  // a split past the current length (device-length launches cover the capacity)
+  const int n = min(kDecSplit, L - k0);
+  u32x4 kw[Ly::NC], vw[Ly::NV];
+  dec_load<D>(p, b, kvh, k0, n, lane, kw, vw);
+  dec_stage_q<D, R>(p, b, kvh, lane, 64, qs);
+  __syncthreads();
+  float m[R], l[R], acc[R][8];
+  dec_split<E, D, R>(p, n, lane, qs, kw, vw, ps, m, l, acc);
+  if (lane / Ly::NC == 0) {
+    const int c = lane;
 #pragma unroll
     for (int h = 0; h < R; ++h) {
       float* dst = p.part + (((int64_t)b * p.Hq + kvh * R + h) * p.nsplit + s) * dec_row<D>();
@@ -198,6 +226,76 @@ __global__ __launch_bounds__(64) void attn_decode_split_kernel(DecodeParams p) {
       *reinterpret_cast<f32x4*>(dst + 8 * c + 4) = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
       if (c == 0) *reinterpret_cast<f32x2*>(dst + D) = f32x2{m[h], l[h]};
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Short caches: split and combine in one launch.
+// ---------------------------------------------------------------------------
+// One workgroup of kDecWaves waves per (batch, KV head); wave w computes split
+// w exactly as the split kernel does, writes its (m, l, o) to LDS, and the
+// workgroup merges the waves with the log-sum-exp rule and writes O: no
+// partials in HBM and no second launch.  The launcher uses it when the cache
+// (its capacity, for device-length launches) holds at most kDecWaves splits,
+// where the split + combine pair is latency-bound.  With more splits per
+// workgroup the B * Hkv workgroups, one per CU, become bound by their CU's
+// VALU and load bandwidth, and the split kernel's grid spread over every CU
+// is faster.
+constexpr int kDecWaves = 8;
+
+template <class E, int D, int R>
+__global__ __launch_bounds__(64 * kDecWaves) void attn_decode_fused_kernel(DecodeParams p) {
+  static_assert(D == 32 || D == 64 || D == 128, "head size");
+  static_assert(R >= 1 && R <= kDecMaxR, "group size");
+  using Ly = DecLayout<D>;
+  __shared__ u32x4 qs[R][Ly::NC];
+  __shared__ float ps[kDecWaves][R][kDecSplit];
+  __shared__ float wo[kDecWaves][R][D];   // the waves' unnormalised o
+  __shared__ float wml[kDecWaves][R][2];  // and (m, l)
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int kvh = blockIdx.x % p.Hkv;
+  const int b = blockIdx.x / p.Hkv;
+  const int L = decode_length(p);
+  const int k0 = wave * kDecSplit;
+  const bool active = k0 < L;  // wave-uniform
+  const int n = min(kDecSplit, L - k0);
+  u32x4 kw[Ly::NC], vw[Ly::NV];
+  if (active) dec_load<D>(p, b, kvh, k0, n, lane, kw, vw);
+  dec_stage_q<D, R>(p, b, kvh, tid, 64 * kDecWaves, qs);
+  __syncthreads();
+  if (active) {
+    float m[R], l[R], acc[R][8];
+    dec_split<E, D, R>(p, n, lane, qs, kw, vw, ps[wave], m, l, acc);
+    if (lane / Ly::NC == 0) {
+      const int c = lane;
+#pragma unroll
+      for (int h = 0; h < R; ++h) {
+        *reinterpret_cast<f32x4*>(&wo[wave][h][8 * c]) = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+        *reinterpret_cast<f32x4*>(&wo[wave][h][8 * c + 4]) = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+        if (c == 0) {
+          wml[wave][h][0] = m[h];
+          wml[wave][h][1] = l[h];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // merge the active waves (0 .. na - 1; wave 0 holds key 0, so na >= 1):
+  // M = max m_w, O = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w
+  const int na = min(kDecWaves, (L + kDecSplit - 1) / kDecSplit);
+  for (int i = tid; i < R * D; i += 64 * kDecWaves) {
+    const int h = i / D, d = i % D;
+    float M = wml[0][h][0];
+    for (int w = 1; w < na; ++w) M = fmaxf(M, wml[w][h][0]);
+    float o = 0.f, lt = 0.f;
+    for (int w = 0; w < na; ++w) {
+      const float a = exp2_fast(wml[w][h][0] - M);
+      o = __builtin_fmaf(a, wo[w][h][d], o);
+      lt = __builtin_fmaf(a, wml[w][h][1], lt);
+    }
+    p.out[b * p.so[0] + (int64_t)(kvh * R + h) * p.so[1] + d] = uint16_t(pack2<E>(o / lt, 0.f) & 0xffffu);
   }
 }
 

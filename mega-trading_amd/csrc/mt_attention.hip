@@ -685,6 +685,22 @@ size_t mt_gqa_attn_decode_workspace_size(int B, int Hq, int L, int D) {
 
 namespace {
 
+// A cache of at most kDecWaves splits of 64 keys (its capacity, for
+// device-length launches) is decoded by the fused kernel, one workgroup per
+// (batch, KV head); longer caches by the split + combine pair, whose grid
+// grows with the length.
+extern "C++" {
+template <class E, int D, int R>
+void launch_decode(const mt::DecodeParams& p, dim3 grid_f, dim3 grid_s, dim3 grid_c, hipStream_t st) {
+  if (p.nsplit <= mt::kDecWaves) {
+    hipLaunchKernelGGL((mt::attn_decode_fused_kernel<E, D, R>), grid_f, dim3(64 * mt::kDecWaves), 0, st, p);
+    return;
+  }
+  hipLaunchKernelGGL((mt::attn_decode_split_kernel<E, D, R>), grid_s, dim3(64), 0, st, p);
+  hipLaunchKernelGGL((mt::attn_decode_combine_kernel<E, D>), grid_c, dim3(256), 0, st, p);
+}
+}  // extern "C++"
+
 int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o, int B, int Hq, int Hkv, int L,
                 const int* length_dev, int D, const int64_t* strides, float scale, int dtype, void* workspace,
                 size_t workspace_bytes, void* stream) {
@@ -717,18 +733,18 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, void* o
   p.nsplit = (L + mt::kDecSplit - 1) / mt::kDecSplit;
   p.scale_log2 = scale * mt::kLog2e;
   hipStream_t st = (hipStream_t)stream;
+  const dim3 grid_f((unsigned)(B * Hkv));
   const dim3 grid_s((unsigned)(B * Hkv * p.nsplit));
   const dim3 grid_c((unsigned)(((int64_t)B * Hq * D + 255) / 256));
-  // the split kernel is instantiated per group size R = Hq / Hkv (1..8)
+  // the decode kernels are instantiated per group size R = Hq / Hkv (1..8)
 #define MT_DECODE_SPLIT(E, DD, RR) \
-  case RR: hipLaunchKernelGGL((mt::attn_decode_split_kernel<E, DD, RR>), grid_s, dim3(64), 0, st, p); break
+  case RR: launch_decode<E, DD, RR>(p, grid_f, grid_s, grid_c, st); break
 #define MT_DECODE_LAUNCH(E, DD)                                                                            \
   switch (p.R) {                                                                                           \
     MT_DECODE_SPLIT(E, DD, 1); MT_DECODE_SPLIT(E, DD, 2); MT_DECODE_SPLIT(E, DD, 3); MT_DECODE_SPLIT(E, DD, 4); \
     MT_DECODE_SPLIT(E, DD, 5); MT_DECODE_SPLIT(E, DD, 6); MT_DECODE_SPLIT(E, DD, 7); MT_DECODE_SPLIT(E, DD, 8); \
     default: break;                                                                                        \
-  }                                                                                                        \
-  hipLaunchKernelGGL((mt::attn_decode_combine_kernel<E, DD>), grid_c, dim3(256), 0, st, p)
+  }
   if (dtype == MT_DTYPE_BF16) {
     if (D == 32) { MT_DECODE_LAUNCH(mt::BF16, 32); } else if (D == 64) { MT_DECODE_LAUNCH(mt::BF16, 64); } else { MT_DECODE_LAUNCH(mt::BF16, 128); }
   } else {

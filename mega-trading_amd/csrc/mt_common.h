@@ -46,6 +46,10 @@ struct BF16 {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3F803F80u),
                                            acc, false);
   }
+  // acc + lo(a) lo(b) + hi(a) hi(b) (v_dot2c_f32_bf16: exact products, fp32 sum)
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+  }
 };
 
 struct FP16 {
@@ -60,6 +64,9 @@ struct FP16 {
   }
   static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
+  }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
   }
 };
 

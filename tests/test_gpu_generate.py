@@ -32,6 +32,12 @@ DECODE_CASES = [
     (1, 32, 8, 4096, 128, torch.bfloat16, 4096),
     (4, 6, 3, 517, 32, torch.float16, 600),
     (32, 8, 2, 1024, 64, torch.bfloat16, 1024),  # BASELINE config 5 layer at the end of the window
+    # up to 16 splits of 64 keys (8 at head_dim 128, group sizes up to 5 there) take the fused
+    # one-launch kernel, longer caches and larger head_dim-128 groups the split + combine pair
+    (2, 8, 2, 1025, 64, torch.bfloat16, 1100),
+    (2, 16, 2, 300, 128, torch.bfloat16, 320),
+    (3, 10, 2, 450, 128, torch.float16, 512),
+    (2, 7, 1, 129, 32, torch.bfloat16, 129),
 ]
 
 
@@ -86,6 +92,25 @@ def test_decode_attention_groups_larger_than_one_launch(hq, hkv, length):
         out = mta.decode_attention(q, kc, vc, ln, repeats=r)
         assert out.shape == (b, hq, 1, d)
         assert np.abs(out[:, :, 0].double().cpu().numpy() - ref).max() <= 2e-2
+
+
+@pytest.mark.parametrize("cap", [1024, 1088])
+def test_decode_device_length_fused_and_split_paths(cap):
+    # a device-side length makes the launch cover the capacity: 16 splits decode in the fused kernel,
+    # 17 in the split + combine pair; every length must give the oracle's row either way
+    g = torch.Generator().manual_seed(cap)
+    b, hq, hkv, d = 3, 8, 2, 64
+    q = (torch.randn(b, hq, 1, d, generator=g) * 0.5).to(torch.bfloat16)
+    kc = (torch.randn(b, hkv, cap, d, generator=g) * 0.5).to(torch.bfloat16)
+    vc = torch.randn(b, hkv, cap, d, generator=g).to(torch.bfloat16)
+    qd, kd, vd = q.cuda(), kc.cuda(), vc.cuda()
+    length = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for ln in (1, 63, 64, 65, 700, 1024, cap):
+        length.fill_(ln)
+        out = mta.decode_attention(qd, kd, vd, length, repeats=hq // hkv)
+        ref = orc.decode_attention(q[:, :, 0].double().numpy(), kc.double().numpy(), vc.double().numpy(), ln,
+                                   hq // hkv)
+        assert np.abs(out[:, :, 0].double().cpu().numpy() - ref).max() <= 2e-2, ln
 
 
 def _model(backend, block_size=64, seed=0, **kw):
