@@ -318,44 +318,28 @@ def time_ops(pkg, iters=20):
 DECODE_SHAPE = (32, 8, 2, 64, 1024)  # C5 generation: rollouts, Hq, Hkv, D, cache capacity (block_size)
 
 
-def time_decode(pkg, lengths=(544, 1024), iters=50):
+DECODE_CASES = ((1024, 544), (1024, 1024), (512, 288), (512, 512))  # (cache capacity, length)
+
+
+def time_decode(pkg, cases=DECODE_CASES, iters=50):
     """One decode step's attention kernels at the config 5 generation shape
-    (32 rollouts, Hq 8, Hkv 2, D 64, a 1024-position bf16 cache), through the
+    (32 rollouts, Hq 8, Hkv 2, D 64, bf16 cache of `capacity` positions:
+    1024 = the config's block_size, and 512 for a shorter window), through the
     C ABI with preallocated buffers, the length read from device memory as the
-    recorded decode step does: the attention (mt_gqa_attn_decode_dev; at this
-    capacity the split + combine pair) and the RoPE / cache-append kernel,
-    each timed over `iters` back-to-back launches with HIP events.
-    Algorithmic bytes: the attention reads the group's q and L cached K and V
-    rows once and writes O; the split + combine pair also writes and reads
-    one fp32 partial (o, m, l) per head and 64-key split (the fused one-launch
-    kernel, used for caches of at most 512 keys, has none); the append reads
-    the fp32 q / k / v projections and writes q_rot and one K and one V cache
-    row."""
+    recorded decode step does: the attention (mt_gqa_attn_decode_dev: the
+    split + combine pair for a 1024-position cache, the fused one-launch
+    kernel for at most 512) and the RoPE / cache-append kernel, each timed
+    over `iters` back-to-back launches with HIP events.  Algorithmic bytes:
+    the attention reads the group's q and L cached K and V rows once and
+    writes O; the split + combine pair also writes and reads one fp32 partial
+    (o, m, l) per head and 64-key split; the append reads the fp32 q / k / v
+    projections and writes q_rot and one K and one V cache row."""
     native = pkg._native
     lib = native.load()
     dev = torch.device("cuda:0")
     sp = torch.cuda.current_stream(dev).cuda_stream
-    b, hq, hkv, d, cap = DECODE_SHAPE
-    g = torch.Generator(device=dev).manual_seed(0)
-    kc = (torch.randn(b, hkv, cap, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
-    vc = (torch.randn(b, hkv, cap, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
-    q = (torch.randn(b, hq, 1, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
-    out = torch.empty_like(q)
-    ws_bytes = lib.mt_gqa_attn_decode_workspace_size(b, hq, cap, d)
-    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
-    st = native.strides_array(q, kc, vc, out)
-    length = torch.zeros(1, device=dev, dtype=torch.int32)
-    # fp32 projections of the new token (generation runs the fp32 model), RoPE tables [cap, D/2]
-    xq = torch.randn(b, hq, 1, d, device=dev, generator=g)
-    xk = torch.randn(b, hkv, 1, d, device=dev, generator=g)
-    xv = torch.randn(b, hkv, 1, d, device=dev, generator=g)
-    cos, sin = rope_tables(cap, d, 10_000.0, dev)
-    q_rot = torch.empty_like(q)
-    ins = (ctypes.c_int64 * 6)(xq.stride(0), xq.stride(1), xk.stride(0), xk.stride(1), xv.stride(0), xv.stride(1))
-    cst = (ctypes.c_int64 * 6)(*kc.stride()[:3], *vc.stride()[:3])
+    b, hq, hkv, d, _ = DECODE_SHAPE
     scale = 1.0 / math.sqrt(d)
-    # the library decodes a cache of at most 8 splits of 64 keys in one fused launch
-    fused = (cap + 63) // 64 <= 8
     res = {}
 
     def timed(fn, n):
@@ -370,8 +354,25 @@ def time_decode(pkg, lengths=(544, 1024), iters=50):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n * 1e3
 
-    for L in lengths:
-        length.fill_(L)
+    for cap, L in cases:
+        g = torch.Generator(device=dev).manual_seed(0)
+        kc = (torch.randn(b, hkv, cap, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        vc = (torch.randn(b, hkv, cap, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        q = (torch.randn(b, hq, 1, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        ws_bytes = lib.mt_gqa_attn_decode_workspace_size(b, hq, cap, d)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+        st = native.strides_array(q, kc, vc, out)
+        length = torch.full((1,), L, device=dev, dtype=torch.int32)
+        # fp32 projections of the new token (generation runs the fp32 model), RoPE tables [cap, D/2]
+        xq = torch.randn(b, hq, 1, d, device=dev, generator=g)
+        xk = torch.randn(b, hkv, 1, d, device=dev, generator=g)
+        xv = torch.randn(b, hkv, 1, d, device=dev, generator=g)
+        cos, sin = rope_tables(cap, d, 10_000.0, dev)
+        q_rot = torch.empty_like(q)
+        ins = (ctypes.c_int64 * 6)(xq.stride(0), xq.stride(1), xk.stride(0), xk.stride(1), xv.stride(0), xv.stride(1))
+        cst = (ctypes.c_int64 * 6)(*kc.stride()[:3], *vc.stride()[:3])
+        fused = (cap + 63) // 64 <= 8  # the library's rule: at most 8 splits of 64 keys in one launch
         ns = (L + 63) // 64
         attn = lambda: native.check(lib.mt_gqa_attn_decode_dev(  # noqa: E731
             q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), b, hq, hkv, cap, length.data_ptr(), d, st,
@@ -380,20 +381,18 @@ def time_decode(pkg, lengths=(544, 1024), iters=50):
             xq.data_ptr(), xk.data_ptr(), xv.data_ptr(), ins, cos.data_ptr(), sin.data_ptr(), cap, L - 1, None,
             q_rot.data_ptr(), kc.data_ptr(), vc.data_ptr(), cst, cap, b, hq, hkv, d, native.DTYPE_FP32,
             native.DTYPE_BF16, sp), "mt_decode_rope_append")
-        kv_bytes = 2 * b * hkv * L * d * 2
-        qo_bytes = 2 * b * hq * d * 2
-        if fused:  # K, V rows 0..L-1, q and out; no partials
-            attn_bytes = kv_bytes + qo_bytes
-        else:  # plus one fp32 partial per head and split, written once and read once
-            attn_bytes = kv_bytes + qo_bytes + 2 * b * hq * ns * (d + 2) * 4
+        attn_bytes = 2 * b * hkv * L * d * 2 + 2 * b * hq * d * 2
+        if not fused:
+            attn_bytes += 2 * b * hq * ns * (d + 2) * 4
         us = timed(attn, iters)
         us_app = timed(append, iters)
         app_bytes = b * (hq + 2 * hkv) * d * 4 + b * (hq + 2 * hkv) * d * 2 + d * 4
-        res[f"L{L}"] = {"attention_us": round(us, 2), "attention_bytes": attn_bytes,
-                        "attention_GBps": round(attn_bytes / (us * 1e-6) / 1e9, 1),
-                        "rope_append_us": round(us_app, 2), "rope_append_bytes": app_bytes}
-    res["attention_kernels"] = "attn_decode_fused_kernel" if fused else "attn_decode_split_kernel + attn_decode_combine_kernel"
-    res["shape"] = "B=32 Hq=8 Hkv=2 D=64 bf16 cache of 1024 positions, length from device memory"
+        res[f"cap{cap}_L{L}"] = {
+            "attention_kernels": "attn_decode_fused_kernel" if fused else "attn_decode_split_kernel + attn_decode_combine_kernel",
+            "attention_us": round(us, 2), "attention_bytes": attn_bytes,
+            "attention_GBps": round(attn_bytes / (us * 1e-6) / 1e9, 1),
+            "rope_append_us": round(us_app, 2), "rope_append_bytes": app_bytes}
+    res["shape"] = "B=32 Hq=8 Hkv=2 D=64 bf16 cache of `cap` positions, length from device memory"
     return res
 
 
