@@ -1600,14 +1600,17 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnParams p) {
 // delta is computed in fp32 from the 16-bit O and dO (triton_attention.py:561);
 // both vectors are stored negated because the dQ and dK/dV passes seed their
 // score and dP accumulators with them.  D/8 lanes per row, each summing one
-// 16-byte chunk, then a butterfly over those lanes.
+// 16-byte chunk, then a DPP butterfly over those lanes.  Every load (O, dO and
+// the row's LSE, which all the row's lanes read) is issued up front: one
+// memory round trip per row.
 template <class E, int D>
 __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(AttnParams p) {
-  constexpr int LPR = D / 8;  // lanes per row
+  constexpr int LPR = D / 8;  // lanes per row: 4, 8 or 16, aligned groups of a 16-lane DPP row
+  static_assert(LPR == 4 || LPR == 8 || LPR == 16, "head size");
   const int64_t rows = (int64_t)p.B * p.Hq * p.T;
   const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
   const int c = threadIdx.x % LPR;
-  float sum = 0.f;
+  float sum = 0.f, lse = 0.f;
   if (row < rows) {
     const int t = int(row % p.T);
     const int64_t bh = row / p.T;
@@ -1616,14 +1619,21 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(AttnParams p) {
     const u32x4 o = *reinterpret_cast<const u32x4*>(p.o + b * p.so[0] + h * p.so[1] + (int64_t)t * p.so[2] + 8 * c);
     const u32x4 g =
         *reinterpret_cast<const u32x4*>(p.dout + b * p.sdo[0] + h * p.sdo[1] + (int64_t)t * p.sdo[2] + 8 * c);
+    lse = p.lse[row];
 #pragma unroll
     for (int w = 0; w < 4; ++w) sum += lo_f<E>(g[w]) * lo_f<E>(o[w]) + hi_f<E>(g[w]) * hi_f<E>(o[w]);
   }
-#pragma unroll
-  for (int m = 1; m < LPR; m <<= 1) sum += __shfl_xor(sum, m, LPR);
+  // sum over the row's lanes: lane ^ 1, lane ^ 2 (quad permutations), then the
+  // mirror within 8 lanes (i <-> 7 - i joins the two quads) and within 16
+  sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xf, 0xf, false));
+  sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xf, 0xf, false));
+  if constexpr (LPR >= 8)
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x141, 0xf, 0xf, false));
+  if constexpr (LPR >= 16)
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x140, 0xf, 0xf, false));
   if (c == 0 && row < rows) {
     p.ndelta[row] = -sum;
-    p.nlse2[row] = -p.lse[row] * kLog2e;
+    p.nlse2[row] = -lse * kLog2e;
   }
 }
 
