@@ -206,7 +206,7 @@ class TradingModel(nn.Module):
                 if step is None:
                     step = _DecodeGraph(self, cache, tokens.shape[0], tokens.device, top_k=top_k)
                     self._gen_state = (key, cache, step)
-                nxt = step(tokens[:, -1:], t - 1)  # the recorded step samples too
+                nxt = step(tokens[:, -1:], t - 1)  # replays the recorded step, then samples
             else:
                 nxt = _sample_next(self._decode(tokens[:, -1:], cache, t - 1), top_k)
             tokens = torch.cat([tokens, nxt], dim=1)
@@ -546,10 +546,14 @@ class _DecodeGraph:
     every position; the host only writes the next token and position before
     each replay.  Replaying a step again for the same position rewrites the
     same cache row with the same values, so the first call (warm-up, record,
-    replay) is harmless.  The result is the graph's static buffer, valid until
-    the next call: the logits, or with ``top_k`` set the sampled next tokens
+    replay) is harmless.  The result is the graph's static logits buffer,
+    valid until the next call, or with ``top_k`` set the sampled next tokens
     [batch, 1] (``_sample_recorded``: the reference's top-k multinomial draw
-    without its host-side validity check, so the sampling is recorded too).
+    without its host-side validity check, so no host synchronisation).  The
+    sampling runs after the replay, outside the recording: ``torch.topk``
+    over a large vocabulary clears its counters with ``hipMemsetAsync``, and
+    memset nodes are kept out of recorded graphs (their replays are not
+    reliable); every recorded kernel writes its outputs in full.
 
     The model is held by a weak reference: the model keeps its recording in
     ``_gen_state``, and a strong reference back would make every generating
@@ -587,12 +591,12 @@ class _DecodeGraph:
                 self.graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(self.graph):
                     self.out = model._decode(self.tok, self.cache, self.pos)
-                    if self.top_k is not None:
-                        self.out = _sample_recorded(self.out, self.top_k)
             finally:
                 if was_enabled:
                     gc.enable()
         self.graph.replay()
+        if self.top_k is not None:
+            return _sample_recorded(self.out, self.top_k)
         return self.out
 
 
@@ -617,7 +621,7 @@ def _sample_next(logits: torch.Tensor, top_k: int) -> torch.Tensor:
 
 
 def _sample_recorded(logits: torch.Tensor, top_k: int) -> torch.Tensor:
-    """``_sample_next`` in a form a HIP graph can record.  For one sample
+    """``_sample_next`` without a host synchronisation.  For one sample
     ``torch.multinomial`` draws argmax(p / E) with E ~ Exponential(1) from the
     same generator, after a host-synchronising check that p holds no inf, NaN
     or negative value; this is that draw without the check (same tokens for

@@ -339,3 +339,21 @@ def test_recorded_sampling_reproduces_the_eager_draw():
     torch.manual_seed(5)
     reused = m.generate(prompt, max_new_tokens=20, top_k=16)
     assert torch.equal(eager, recorded) and torch.equal(recorded, reused)
+
+
+def test_recorded_decode_with_a_large_vocabulary_samples_like_the_eager_step():
+    # over a 16 k vocabulary torch.topk takes its multi-block path, which clears counters with
+    # hipMemsetAsync; the sampling therefore runs after each replay, outside the recording.  32 rollouts
+    # x 24 tokens with the recorded step (recording call and reuse) against the eager step, same seed
+    g = torch.Generator().manual_seed(41)
+    m = _model("hip", block_size=64, vocab_size=16384, hidden_dim=128, attention_heads=4, kv_heads=1)
+    prompt = torch.randint(0, 16384, (32, 12), generator=g).cuda()
+    torch.manual_seed(3)
+    m.decode_graphs = False
+    eager = m.generate(prompt, max_new_tokens=24, top_k=16)
+    m.decode_graphs = True
+    for _ in range(2):
+        torch.manual_seed(3)
+        recorded = m.generate(prompt, max_new_tokens=24, top_k=16)
+        torch.cuda.synchronize()
+        assert torch.equal(recorded, eager)
