@@ -29,6 +29,10 @@
  *                           _rope_kernel :690-761, launcher :477-525), reached
  *                           from triton_apply_rope :45-54 and
  *                           RotaryEmbedding.forward, src/mega_trading/model.py:292-293
+ *   mt_linear_rows       <- the bias-free nn.Linear products of the decoder
+ *                           (src/mega_trading/model.py:209-212, 243-245; applied at
+ *                           :220-222, :237, :250-256) for the few rows of a decode
+ *                           step (one token per rollout), several weights per launch
  *   mt_cross_entropy_rows <- _fused_ce_row_kernel :822-887, the per-chunk loss and
  *                           in-place logits-gradient step of
  *                           _TritonFusedLinearCrossEntropy.forward :312-400,
@@ -160,6 +164,22 @@ int mt_cross_entropy_rows(void* logits, int64_t row_stride, const int64_t* label
 int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B, int Hq, int Hkv, int T, int D,
                   const int64_t* strides, const float* rope_cos, const float* rope_sin, int64_t table_stride,
                   int table_rows, int inverse, int dtype, void* stream);
+
+/* Products of a few rows against grouped weights, fp32:
+ *   y[m, off_g + n] = sum_k x[m, k] w_g[n, k],  off_g = out_features[0] + ... + out_features[g-1],
+ * for m < rows, n < out_features[g], g < groups: the bias-free nn.Linear of each
+ * weight w_g [out_features[g], in_features] (row stride w_row_strides[g]), the
+ * results side by side in y's rows (y row stride y_row_stride >= the sum of
+ * out_features).  `weights` and `out_features`, `w_row_strides` are host arrays
+ * (device pointers in `weights`).  x is [rows, in_features] with row stride
+ * x_row_stride.  One launch reads every weight in place (no concatenation): the
+ * decode step's q|k|v and w1|w3 projections.  dtype MT_DTYPE_FP32 only;
+ * 1 <= groups <= 4; 1 <= rows <= 64; in_features a positive multiple of 128;
+ * x and the weights 16-byte aligned with row strides that are multiples of 4.
+ * Sums in fp32 (MFMA), in an order of this kernel's own. */
+int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weights, const int* out_features,
+                   const int64_t* w_row_strides, int groups, void* y, int64_t y_row_stride, int rows, int in_features,
+                   int dtype, void* stream);
 
 #ifdef __cplusplus
 }

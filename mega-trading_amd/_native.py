@@ -52,6 +52,7 @@ EXPORTS = (
     "mt_gqa_attn_decode",
     "mt_gqa_attn_decode_dev",
     "mt_decode_rope_append",
+    "mt_linear_rows",
 )
 
 _lock = threading.Lock()
@@ -87,6 +88,7 @@ _OPS_SIGNATURES = {
     "mt_gqa_attn_decode_dev": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _F, _I, _P, _S, _P]),
     "mt_decode_rope_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
                                    _P]),
+    "mt_linear_rows": (_I, [_P, _L, _P, _P, _P, _I, _P, _L, _I, _I, _I, _P]),
 }
 
 

@@ -1,0 +1,111 @@
+// gfx950 fp32 products of a few rows against grouped weights: the decode
+// step's projections.  y[m, off_g + n] = sum_k x[m, k] w_g[n, k] for every
+// group g (the q, k and v projections of a layer, or its w1 and w3), from one
+// launch that reads each weight matrix where it lies: the "hip" decoder's
+// packed GEMM otherwise concatenates the weights first (a copy of every
+// weight per call), and the library GEMMs at 32 rows are latency-bound.
+//
+// One workgroup per 16 x 16 tile of y (16 rows, 16 columns of one group),
+// 8 waves; the contraction is cut into 32 segments of K / 32 values, wave w
+// and lane quarter q taking segment 4 w + q.  A lane loads its segment of one
+// x row and one w row as 16-byte chunks, all of them before the first product
+// (up to 12 chunks: one memory round trip for K <= 1536), and feeds them to
+// v_mfma_f32_16x16x4_f32, whose contraction slot is the lane quarter, so the
+// four quarters' partial sums add inside the MFMA; the 8 waves' tiles are
+// summed through LDS.  Row tiles are separate workgroups so that narrow
+// outputs (512 columns: 32 column tiles) still spread over 64 or more CUs.
+// fp32 throughout (the reference's eval runs the fp32 model without
+// autocast).
+#pragma once
+
+#include "mt_common.h"
+
+namespace mt {
+
+constexpr int kLinGroups = 4;   // weight groups per launch
+constexpr int kLinWaves = 8;
+constexpr int kLinCols = 16;    // columns per workgroup
+constexpr int kLinMaxRows = 64; // rows per launch (four 16-row tiles)
+
+struct LinearGroup {
+  const float* w;   // [n, K], row stride ldw
+  int64_t ldw;
+  int n;            // output columns of the group
+  int col_off;      // first column of the group in y
+  int tile0;        // first workgroup of the group
+};
+
+struct LinearParams {
+  const float* x;   // [M, K], row stride ldx
+  float* y;         // [M, >= sum n], row stride ldy
+  int64_t ldx, ldy;
+  int M, K, groups;
+  LinearGroup g[kLinGroups];
+};
+
+// MFMA layout (16x16x4, fp32): A[i][k] from lane i + 16 k, B[k][j] from lane
+// j + 16 k; lane l holds D[4 (l / 16) + v][l % 16], v = 0..3.
+// PD: 16-byte chunks per lane held in flight (all of them when K <= 128 PD).
+template <int PD>
+__global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearParams p) {
+  __shared__ float red[kLinWaves][16][17];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int q = lane >> 4;   // contraction slot
+  const int c = lane & 15;   // A row / B column of this lane
+  const int ntiles = p.g[p.groups - 1].tile0 + (p.g[p.groups - 1].n + kLinCols - 1) / kLinCols;
+  const int ct = (int)blockIdx.x % ntiles;  // column tile
+  const int m0 = ((int)blockIdx.x / ntiles) * 16;
+  int gi = 0;
+#pragma unroll
+  for (int i = 1; i < kLinGroups; ++i)
+    if (i < p.groups && ct >= p.g[i].tile0) gi = i;
+  const LinearGroup grp = p.g[gi];
+  const int n0 = (ct - grp.tile0) * kLinCols;
+
+  // this lane's segment of the contraction: S = K / 32 values, S % 4 == 0
+  const int S = p.K >> 5;
+  const int k0 = (4 * wave + q) * S;
+  const float* wrow = grp.w + (int64_t)min(n0 + c, grp.n - 1) * grp.ldw + k0;
+  const float* xrow = p.x + (int64_t)min(m0 + c, p.M - 1) * p.ldx + k0;
+
+  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // two chains: back-to-back issue
+  const int nch = S >> 2;
+  f32x4 wb[PD], xb[PD];
+#pragma unroll
+  for (int j = 0; j < PD; ++j)
+    if (j < nch) {
+      wb[j] = *reinterpret_cast<const f32x4*>(wrow + 4 * j);
+      xb[j] = *reinterpret_cast<const f32x4*>(xrow + 4 * j);
+    }
+  for (int i0 = 0; i0 < nch; i0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; ++j) {
+      const int i = i0 + j;
+      if (i < nch) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[e & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[j][e], wb[j][e], acc[e & 1], 0, 0, 0);
+        if (i + PD < nch) {
+          wb[j] = *reinterpret_cast<const f32x4*>(wrow + 4 * (i + PD));
+          xb[j] = *reinterpret_cast<const f32x4*>(xrow + 4 * (i + PD));
+        }
+      }
+    }
+  }
+  // the waves' tiles through LDS, then one output per thread of the first 4 waves
+#pragma unroll
+  for (int v = 0; v < 4; ++v) red[wave][4 * q + v][c] = acc[0][v] + acc[1][v];
+  __syncthreads();
+  if (tid < 256) {
+    const int r = tid >> 4, col = tid & 15;
+    const int m = m0 + r, n = n0 + col;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kLinWaves; ++w) s += red[w][r][col];
+    if (m < p.M && n < grp.n) p.y[(int64_t)m * p.ldy + grp.col_off + n] = s;
+  }
+}
+
+}  // namespace mt

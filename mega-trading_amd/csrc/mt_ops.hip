@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "../../include/mt_ops.h"
+#include "linear_kernels.h"
 #include "mt_abi.h"
 #include "ops_kernels.h"
 
@@ -524,6 +525,58 @@ int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B,
   if (dtype == MT_DTYPE_BF16) rope_launch<K::kDtBF16>(vec, grid, st, a);
   else if (dtype == MT_DTYPE_FP16) rope_launch<K::kDtFP16>(vec, grid, st, a);
   else rope_launch<K::kDtFP32>(vec, grid, st, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weights, const int* out_features,
+                   const int64_t* w_row_strides, int groups, void* y, int64_t y_row_stride, int rows, int in_features,
+                   int dtype, void* stream) {
+  if (dtype != MT_DTYPE_FP32) return fail(MT_E_DTYPE, "dtype code %d unsupported (fp32 only)", dtype);
+  if (groups < 1 || groups > mt::kLinGroups)
+    return fail(MT_E_SHAPE, "groups must be in [1, %d] (got %d)", mt::kLinGroups, groups);
+  if (rows < 1 || rows > mt::kLinMaxRows)
+    return fail(MT_E_SHAPE, "rows must be in [1, %d] (got %d)", mt::kLinMaxRows, rows);
+  if (in_features < 128 || in_features % 128)
+    return fail(MT_E_SHAPE, "in_features must be a positive multiple of 128 (got %d)", in_features);
+  if (!weights || !out_features || !w_row_strides) return fail(MT_E_NULL, "weights, out_features or w_row_strides is NULL");
+  int rc;
+  if ((rc = check_ptr("x", x))) return rc;
+  if (!y) return fail(MT_E_NULL, "y is NULL");
+  if (x_row_stride < in_features || x_row_stride % 4)
+    return fail(MT_E_STRIDE, "x row stride %lld must be >= in_features and a multiple of 4", (long long)x_row_stride);
+  mt::LinearParams p{};
+  p.x = static_cast<const float*>(x);
+  p.y = static_cast<float*>(y);
+  p.ldx = x_row_stride;
+  p.ldy = y_row_stride;
+  p.M = rows;
+  p.K = in_features;
+  p.groups = groups;
+  int64_t cols = 0, tiles = 0;
+  for (int g = 0; g < groups; ++g) {
+    if ((rc = check_ptr("weights[g]", weights[g]))) return rc;
+    if (out_features[g] < 1) return fail(MT_E_SHAPE, "out_features[%d] must be >= 1 (got %d)", g, out_features[g]);
+    if (w_row_strides[g] < in_features || w_row_strides[g] % 4)
+      return fail(MT_E_STRIDE, "weight %d row stride %lld must be >= in_features and a multiple of 4", g,
+                  (long long)w_row_strides[g]);
+    p.g[g].w = static_cast<const float*>(weights[g]);
+    p.g[g].ldw = w_row_strides[g];
+    p.g[g].n = out_features[g];
+    p.g[g].col_off = (int)cols;
+    p.g[g].tile0 = (int)tiles;
+    cols += out_features[g];
+    tiles += (out_features[g] + mt::kLinCols - 1) / mt::kLinCols;
+  }
+  if (cols > 0x7fffffffLL) return fail(MT_E_SHAPE, "too many output columns (%lld)", (long long)cols);
+  if (y_row_stride < cols) return fail(MT_E_STRIDE, "y row stride %lld must be >= %lld", (long long)y_row_stride,
+                                       (long long)cols);
+  if (tiles * ((rows + 15) / 16) > 0x7fffffffLL) return fail(MT_E_SHAPE, "too many output tiles");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)(tiles * ((rows + 15) / 16))), block(64 * mt::kLinWaves);
+  // every chunk of a lane in flight at once up to K = 1536 (12 chunks of 4 values per lane)
+  if (in_features <= 128 * 12) hipLaunchKernelGGL((mt::linear_rows_f32_kernel<12>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((mt::linear_rows_f32_kernel<4>), grid, block, 0, st, p);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }

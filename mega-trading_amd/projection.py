@@ -10,6 +10,12 @@ autocast: inside a CUDA autocast region the product runs in the autocast
 dtype, otherwise in the promoted dtype of ``x`` and the weights; the
 parameters stay in their own dtype and get gradients of that dtype.
 
+Few rows without autograd (the decode step of generation: one token per
+rollout, at most 64 rows, fp32 as the reference's eval runs the model):
+``mt_linear_rows`` computes the packed result in one launch that reads every
+weight in place, instead of concatenating the weights (a copy of each weight
+per call) and running a library GEMM that is latency-bound at these sizes.
+
 Backward:
 * dX = dY W: one GEMM over the packed gradient.
 * dW = dYᵀ X reduces over every token (batch x time rows, 32768 at the
@@ -24,10 +30,12 @@ Backward:
 
 from __future__ import annotations
 
+import ctypes
 from typing import Sequence
 
 import torch
 
+from . import _native
 from .gemm_tuning import tuned_gemms
 
 __all__ = ["project", "project_packed", "split_k_chunks"]
@@ -105,6 +113,51 @@ class _Project(torch.autograd.Function):
         return (dx, None, *dws)
 
 
+_ROWS_MAX = 64     # rows of one mt_linear_rows launch
+_ROWS_GROUPS = 4   # weights of one launch
+
+
+def _rows_path(x2: torch.Tensor, weights: Sequence[torch.Tensor], dtype: torch.dtype) -> bool:
+    """Whether ``mt_linear_rows`` takes the product: no autograd, fp32 operands
+    and compute, at most 64 rows and 4 weights, in_features a multiple of 128,
+    16-byte aligned rows with unit last strides."""
+    if dtype != torch.float32 or x2.dtype != torch.float32 or x2.device.type != "cuda":
+        return False
+    if torch.is_grad_enabled() and (x2.requires_grad or any(w.requires_grad for w in weights)):
+        return False
+    rows, k = x2.shape
+    if not 1 <= rows <= _ROWS_MAX or k % 128 or len(weights) > _ROWS_GROUPS:
+        return False
+    if x2.stride(1) != 1 or x2.stride(0) % 4 or x2.data_ptr() % 16:
+        return False
+    return all(w.dtype == torch.float32 and w.device == x2.device and w.stride(1) == 1 and w.stride(0) % 4 == 0
+               and w.data_ptr() % 16 == 0 for w in weights)
+
+
+@torch.library.custom_op("mega_trading_amd::linear_rows", mutates_args=(), device_types="cuda")
+def linear_rows(x: torch.Tensor, weights: list[torch.Tensor]) -> torch.Tensor:
+    """[rows, sum(out_i)] = cat([x @ w.T for w in weights], -1) for fp32 x
+    [rows <= 64, K] and weights [out_i, K] (``mt_linear_rows``)."""
+    lib = _native.load()
+    rows, k = x.shape
+    outs = [w.shape[0] for w in weights]
+    y = torch.empty((rows, sum(outs)), device=x.device, dtype=torch.float32)
+    g = len(weights)
+    ptrs = (ctypes.c_void_p * g)(*[w.data_ptr() for w in weights])
+    ns = (ctypes.c_int * g)(*outs)
+    lds = (ctypes.c_int64 * g)(*[w.stride(0) for w in weights])
+    with torch.cuda.device(x.device):
+        rc = lib.mt_linear_rows(x.data_ptr(), x.stride(0), ptrs, ns, lds, g, y.data_ptr(), y.stride(0), rows, k,
+                                _native.DTYPE_FP32, torch.cuda.current_stream(x.device).cuda_stream)
+    _native.check(rc, "mt_linear_rows")
+    return y
+
+
+@linear_rows.register_fake
+def _linear_rows_fake(x, weights):
+    return x.new_empty((x.shape[0], sum(w.shape[0] for w in weights)))
+
+
 def _check(x: torch.Tensor, weights: Sequence[torch.Tensor]) -> None:
     if not weights:
         raise ValueError("weights must hold at least one matrix")
@@ -119,7 +172,11 @@ def _check(x: torch.Tensor, weights: Sequence[torch.Tensor]) -> None:
 def project_packed(x: torch.Tensor, weights: Sequence[torch.Tensor]) -> torch.Tensor:
     """``cat([x @ w.T for w in weights], -1)`` from one GEMM: [..., sum(out_i)]."""
     _check(x, weights)
-    return _Project.apply(x, _compute_dtype(x, weights), *weights)
+    dtype = _compute_dtype(x, weights)
+    x2 = x.reshape(-1, x.shape[-1])
+    if _rows_path(x2, weights, dtype):
+        return linear_rows(x2, list(weights)).view(*x.shape[:-1], -1)
+    return _Project.apply(x, dtype, *weights)
 
 
 def project(x: torch.Tensor, weights: Sequence[torch.Tensor]) -> tuple[torch.Tensor, ...]:

@@ -129,6 +129,25 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     assert lib.mt_apply_rope(p, p, p, p, 1, 4, 2, 8, 64, st, p, p, 32, 8, 0, 9, None) == -4
     assert lib.mt_apply_rope(p, p, p, p, -1, 4, 2, 8, 64, st, p, p, 32, 8, 0, BF16, None) == -2
     assert lib.mt_apply_rope(None, None, None, None, 0, 4, 2, 8, 64, None, None, None, 32, 8, 0, BF16, None) == 0
+    # few-row products against grouped weights: fp32, 1..4 groups, 1..64 rows, K a multiple of 128
+    ws = (ctypes.c_void_p * 2)(p, p)
+    ns = (ctypes.c_int * 2)(64, 32)
+    ld = (ctypes.c_int64 * 2)(512, 512)
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 32, 512, BF16, None) == -4
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 0, p, 96, 32, 512, FP32, None) == -2
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 5, p, 96, 32, 512, FP32, None) == -2
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 65, 512, FP32, None) == -2
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 0, 512, FP32, None) == -2
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 32, 500, FP32, None) == -2
+    assert b"multiple of 128" in lib.mt_last_error()
+    assert lib.mt_linear_rows(p + 4, 512, ws, ns, ld, 2, p, 96, 32, 512, FP32, None) == -3  # misaligned x
+    assert lib.mt_linear_rows(p, 510, ws, ns, ld, 2, p, 96, 32, 512, FP32, None) == -3  # x stride < K
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 95, 32, 512, FP32, None) == -3  # y stride < 96 columns
+    assert lib.mt_linear_rows(p, 512, ws, ns, (ctypes.c_int64 * 2)(512, 514), 2, p, 96, 32, 512, FP32, None) == -3
+    assert lib.mt_linear_rows(p, 512, (ctypes.c_void_p * 2)(p, p + 8), ns, ld, 2, p, 96, 32, 512, FP32, None) == -3
+    assert lib.mt_linear_rows(p, 512, ws, (ctypes.c_int * 2)(64, 0), ld, 2, p, 96, 32, 512, FP32, None) == -2
+    assert lib.mt_linear_rows(p, 512, None, ns, ld, 2, p, 96, 32, 512, FP32, None) == -1
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, None, 96, 32, 512, FP32, None) == -1
 
 
 def test_ops_reject_cpu_tensors(mta):
@@ -308,6 +327,9 @@ def test_fake_impls_give_shapes_for_tracing(mta):
         assert o3.shape == (2, 100, 512) and l3.shape == (2, 8, 100) and qr3.shape == q.shape and kr3.shape == k.shape
         d3 = torch.ops.mega_trading_amd.gqa_attn_bwd_packed(qr3, kr3, qkv, o3, l3, o3, cs, cs, 8, 2, 0.125)
         assert d3.shape == qkv.shape
+        y = torch.ops.mega_trading_amd.linear_rows(_fake((32, 512), torch.float32),
+                                                   [_fake((768, 512), torch.float32), _fake((64, 512), torch.float32)])
+        assert y.shape == (32, 832) and y.dtype == torch.float32
 
 
 def test_kernel_ready_keeps_model_layout_views():
