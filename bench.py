@@ -9,11 +9,12 @@
   14 * B * Hq * D * T(T+1)/2 (scripts/benchmark_triton_attention.py:179-190
   gives the forward 4 * B * Hq * D * T(T+1)/2; backward adds 2.5x).
 * roofline: the dominant kernel's (the one-launch backward's) algorithmic
-  MFMA FLOPs per launch over its average duration within the headline's own
-  timed windows, from HIP events that the library attaches to each of its
-  dispatches (mt_time_kernel_queue; the backward runs on the autograd
-  engine's thread) on the launch stream; traffic is its HBM bytes per launch
-  from the committed rocprofv3 counter summary.
+  MFMA FLOPs per launch over its average duration in a second set of the
+  headline's timed windows (the same steps right after them), from HIP
+  events that the library attaches to each of its dispatches
+  (mt_time_kernel_queue; the backward runs on the autograd engine's thread)
+  on the launch stream; traffic is its HBM bytes per launch from the
+  committed rocprofv3 counter summary.
 * cpu_baseline: the reference's CPU attention path (torch SDPA, fp32, forward
   + autograd backward, model.py:228-235) on the host cores over a bounded
   sample of the same workload.
@@ -121,10 +122,12 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s
     window bracketed by synchronisation and HIP events on the current stream.
     Returns ms per step: median, fastest and slowest window, the cold
     window, and the median window's wall-clock time per step.  kernel_events:
-    also the average duration of the step's two main kernels (the forward and
-    the backward launch) over those windows, from HIP events the library
-    attaches to each of their dispatches (mt_time_kernel_queue: the backward
-    is launched from the autograd engine's thread)."""
+    then `repeats` more windows of the same steps with HIP events that the
+    library attaches to each dispatch of the step's two main kernels (the
+    forward and the backward launch; mt_time_kernel_queue, since the backward
+    is launched from the autograd engine's thread), giving their average
+    durations and those windows' median ms per step (the events add about
+    2 % to a step, so the plain windows give `ms`)."""
     b, t, hq, hkv, d = cfg
     dev = torch.device("cuda:0")
     q, k, v, do = make_inputs(cfg, dev)
@@ -160,8 +163,13 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s
             step()
         n += 8
         torch.cuda.synchronize()
-    ev = None
+    runs = sorted(window() for _ in range(repeats))
+    med_ms, med_wall = runs[len(runs) // 2]
+    res = {"ms": med_ms, "ms_min": runs[0][0], "ms_max": runs[-1][0], "ms_cold": cold, "wall_ms": med_wall,
+           "repeats": repeats, "warmup_steps": n}
     if kernel_events:
+        # the same windows again with events on each kernel dispatch (they add
+        # about 2 % to a step, so `ms` comes from the plain windows above)
         lib = pkg._native.load()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(2 * steps * repeats)]
@@ -173,12 +181,9 @@ def time_op_steps(pkg, cfg, steps, warmup, rope=True, repeats=REPEATS, preheat_s
         pkg._native.check(lib.mt_time_kernel_queue(arr(*[a.cuda_event for a, _ in ev]),
                                                    arr(*[b_.cuda_event for _, b_ in ev]), len(ev)),
                           "mt_time_kernel_queue")
-    runs = sorted(window() for _ in range(repeats))
-    med_ms, med_wall = runs[len(runs) // 2]
-    res = {"ms": med_ms, "ms_min": runs[0][0], "ms_max": runs[-1][0], "ms_cold": cold, "wall_ms": med_wall,
-           "repeats": repeats, "warmup_steps": n}
-    if ev is not None:
+        inst = sorted(window() for _ in range(repeats))
         pkg._native.check(lib.mt_time_kernel_queue(None, None, 0), "mt_time_kernel_queue")
+        res["ms_instrumented"] = inst[len(inst) // 2][0]
         res["fwd_kernel_ms"] = sum(a.elapsed_time(b_) for a, b_ in ev[0::2]) / (len(ev) // 2)
         res["bwd_kernel_ms"] = sum(a.elapsed_time(b_) for a, b_ in ev[1::2]) / (len(ev) // 2)
     return res
@@ -850,7 +855,8 @@ def main(argv=None) -> int:
     tflops = lambda ms: round(flops / (ms * 1e-3) / 1e12, 2)  # noqa: E731
 
     # the dominant kernel: the one-launch backward; its duration is averaged
-    # over the headline's own timed windows (events on each of its dispatches)
+    # over the headline's instrumented windows (the same steps, timed right
+    # after the plain windows, with events on each of its dispatches)
     kern = time_kernels(pkg, C3, max(10, args.steps // 2))
     dom = "attn_bwd_kernel"
     unit_flop = b * hq * d * pairs(t)
@@ -882,6 +888,8 @@ def main(argv=None) -> int:
             "ms_cold_window": round(head["ms_cold"], 4), "tflops_cold_window": tflops(head["ms_cold"]),
             "fwd_kernel_ms_in_windows": round(head["fwd_kernel_ms"], 4),
             "bwd_kernel_ms_in_windows": round(head["bwd_kernel_ms"], 4),
+            "kernel_windows": f"{head['repeats']} further windows of the same steps with HIP events on each "
+                              f"forward and backward dispatch (median {head['ms_instrumented']:.4f} ms per step)",
         },
         "higher_is_better": True,
         "scaling": "weak",
