@@ -33,6 +33,9 @@
  *                           (src/mega_trading/model.py:209-212, 243-245; applied at
  *                           :220-222, :237, :250-256) for the few rows of a decode
  *                           step (one token per rollout), several weights per launch
+ *   mt_topk_sample       <- the top-k draw of TradingModel.generate
+ *                           (src/mega_trading/model.py:141-145: topk, masked_fill,
+ *                           softmax, multinomial for one sample) in one launch
  *   mt_cross_entropy_rows <- _fused_ce_row_kernel :822-887, the per-chunk loss and
  *                           in-place logits-gradient step of
  *                           _TritonFusedLinearCrossEntropy.forward :312-400,
@@ -180,6 +183,17 @@ int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B,
 int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weights, const int* out_features,
                    const int64_t* w_row_strides, int groups, void* y, int64_t y_row_stride, int rows, int in_features,
                    int dtype, void* stream);
+
+/* One sampled token per row: the logits >= the k-th largest of the row are
+ * kept (ties at the k-th value included), p = softmax over the kept values,
+ * and tokens[r] = the first index of the largest p / E[r, i] over the kept i,
+ * with E the caller's Exponential(1) noise (one value per logit, e.g. drawn by
+ * torch's exponential_ from its generator): the draw torch.multinomial makes for
+ * one sample, without its host-side validity check.  logits and noise are fp32
+ * [rows, vocab] with row strides >= vocab; tokens int64 [rows].  dtype
+ * MT_DTYPE_FP32; 1 <= vocab <= 32768; 1 <= k <= vocab; rows >= 0. */
+int mt_topk_sample(const void* logits, int64_t row_stride, const void* noise, int64_t noise_row_stride, int rows,
+                   int vocab, int k, int64_t* tokens, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -53,6 +53,7 @@ EXPORTS = (
     "mt_gqa_attn_decode_dev",
     "mt_decode_rope_append",
     "mt_linear_rows",
+    "mt_topk_sample",
 )
 
 _lock = threading.Lock()
@@ -89,6 +90,7 @@ _OPS_SIGNATURES = {
     "mt_decode_rope_append": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
                                    _P]),
     "mt_linear_rows": (_I, [_P, _L, _P, _P, _P, _I, _P, _L, _I, _I, _I, _P]),
+    "mt_topk_sample": (_I, [_P, _L, _P, _L, _I, _I, _I, _P, _I, _P]),
 }
 
 

@@ -49,34 +49,6 @@ __device__ __forceinline__ int decode_length(const DecodeParams& p) {
   return p.length_dev ? min(max(*p.length_dev, 1), p.L) : p.L;
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
-template <bool MAX>
-__device__ __forceinline__ float red_op(float a, float b) {
-  return MAX ? fmaxf(a, b) : a + b;
-}
-
-// Max or sum over lane bits [LO, 6) of a wave64; every lane receives the
-// result.  Bits 0-1: quad permutations; bits 2-3: row rotations by 4 and 8
-// (after them each lane holds the sum over the lanes of its row that agree
-// with it in the lower bits); bits 4-5: v_permlane16/32_swap.
-template <int LO, bool MAX>
-__device__ __forceinline__ float wave_reduce(float x) {
-  if constexpr (LO <= 0) x = red_op<MAX>(x, dpp_mov<0xB1>(x));   // quad_perm(1,0,3,2): lane ^ 1
-  if constexpr (LO <= 1) x = red_op<MAX>(x, dpp_mov<0x4E>(x));   // quad_perm(2,3,0,1): lane ^ 2
-  if constexpr (LO <= 2) x = red_op<MAX>(x, dpp_mov<0x124>(x));  // row_ror:4
-  if constexpr (LO <= 3) x = red_op<MAX>(x, dpp_mov<0x128>(x));  // row_ror:8
-  if constexpr (LO <= 4) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  }
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 // q . k of one cached row for each of the R heads: two products per
 // v_dot2c_f32 (exact 16-bit products, fp32 sums) straight from the stored
 // pairs, with no conversion of k.

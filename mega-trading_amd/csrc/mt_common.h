@@ -85,6 +85,35 @@ __device__ __forceinline__ float hi_f(uint32_t w) { return E::to_f(uint16_t(w >>
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <bool MAX>
+__device__ __forceinline__ float red_op(float a, float b) {
+  return MAX ? fmaxf(a, b) : a + b;
+}
+
+// Max or sum over lane bits [LO, 6) of a wave64; every lane receives the
+// result.  Bits 0-1: quad permutations; bits 2-3: row rotations by 4 and 8
+// (after them each lane holds the sum over the lanes of its row that agree
+// with it in the lower bits); bits 4-5: v_permlane16/32_swap.
+template <int LO, bool MAX>
+__device__ __forceinline__ float wave_reduce(float x) {
+  if constexpr (LO <= 0) x = red_op<MAX>(x, dpp_mov<0xB1>(x));   // quad_perm(1,0,3,2): lane ^ 1
+  if constexpr (LO <= 1) x = red_op<MAX>(x, dpp_mov<0x4E>(x));   // quad_perm(2,3,0,1): lane ^ 2
+  if constexpr (LO <= 2) x = red_op<MAX>(x, dpp_mov<0x124>(x));  // row_ror:4
+  if constexpr (LO <= 3) x = red_op<MAX>(x, dpp_mov<0x128>(x));  // row_ror:8
+  if constexpr (LO <= 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return red_op<MAX>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+
 // Max of a value and its lane^32 partner (both halves of the wave end up equal).
 __device__ __forceinline__ float max_with_partner(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -10,6 +10,7 @@
 #include "linear_kernels.h"
 #include "mt_abi.h"
 #include "ops_kernels.h"
+#include "sample_kernels.h"
 
 namespace {
 
@@ -579,6 +580,32 @@ int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weigh
   else hipLaunchKernelGGL((mt::linear_rows_f32_kernel<4>), grid, block, 0, st, p);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
+}
+
+int mt_topk_sample(const void* logits, int64_t row_stride, const void* noise, int64_t noise_row_stride, int rows,
+                   int vocab, int k, int64_t* tokens, int dtype, void* stream) {
+  if (dtype != MT_DTYPE_FP32) return fail(MT_E_DTYPE, "dtype code %d unsupported (fp32 only)", dtype);
+  if (rows < 0) return fail(MT_E_SHAPE, "rows must be >= 0 (got %d)", rows);
+  if (vocab < 1 || vocab > 32 * mt::kSampleThreads)
+    return fail(MT_E_SHAPE, "vocab must be in [1, %d] (got %d)", 32 * mt::kSampleThreads, vocab);
+  if (k < 1 || k > vocab) return fail(MT_E_SHAPE, "k must be in [1, vocab] (got %d)", k);
+  if (row_stride < vocab || noise_row_stride < vocab)
+    return fail(MT_E_STRIDE, "row strides (%lld, %lld) must be >= vocab", (long long)row_stride,
+                (long long)noise_row_stride);
+  if (rows == 0) return ok();
+  if (!logits || !noise || !tokens) return fail(MT_E_NULL, "logits, noise or tokens is NULL");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)rows), block(mt::kSampleThreads);
+  const float* x = static_cast<const float*>(logits);
+  const float* e = static_cast<const float*>(noise);
+  if (vocab <= 8 * mt::kSampleThreads)
+    hipLaunchKernelGGL((mt::topk_sample_kernel<8>), grid, block, 0, st, x, row_stride, e, noise_row_stride, vocab, k, tokens);
+  else if (vocab <= 16 * mt::kSampleThreads)
+    hipLaunchKernelGGL((mt::topk_sample_kernel<16>), grid, block, 0, st, x, row_stride, e, noise_row_stride, vocab, k, tokens);
+  else
+    hipLaunchKernelGGL((mt::topk_sample_kernel<32>), grid, block, 0, st, x, row_stride, e, noise_row_stride, vocab, k, tokens);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? ok() : fail((int)err, "launch failed: %s", hipGetErrorString(err));
 }
 
 }  // extern "C"

@@ -55,6 +55,8 @@ from .ops import rms_norm as _hip_rms_norm
 from .ops import rms_norm_mixed as _hip_rms_norm_mixed
 from .ops import swiglu_gate as _hip_swiglu_gate
 from .ops import swiglu_gate_packed as _hip_swiglu_gate_packed
+from .ops import MAX_SAMPLE_VOCAB as _MAX_SAMPLE_VOCAB
+from .ops import topk_sample as _hip_topk_sample
 from .projection import project as _project
 from .projection import project_packed as _project_packed
 
@@ -625,7 +627,14 @@ def _sample_recorded(logits: torch.Tensor, top_k: int) -> torch.Tensor:
     ``torch.multinomial`` draws argmax(p / E) with E ~ Exponential(1) from the
     same generator, after a host-synchronising check that p holds no inf, NaN
     or negative value; this is that draw without the check (same tokens for
-    the same generator state)."""
+    the same generator state).  For fp32 GPU logits it is one HIP launch
+    (``ops.topk_sample``) after the same noise draw; the kernel's fp32 sums
+    run in its own order, so only a p / E tie within a rounding error could
+    pick another token than the library kernels."""
+    k = min(top_k, logits.shape[-1])
+    if (top_k > 0 and logits.is_cuda and logits.dtype == torch.float32 and logits.ndim == 2
+            and logits.shape[-1] <= _MAX_SAMPLE_VOCAB):
+        return _hip_topk_sample(logits, torch.empty_like(logits).exponential_(1), k)
     if top_k > 0:
         values, _ = torch.topk(logits, min(top_k, logits.shape[-1]))
         logits = logits.masked_fill(logits < values[:, -1:], float("-inf"))  # a slice: no host index tensor

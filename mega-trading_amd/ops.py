@@ -31,9 +31,10 @@ from . import _native
 from .gemm_tuning import tuned_gemms
 
 __all__ = ["rms_norm", "add_rms_norm", "rms_norm_mixed", "add_rms_norm_mixed", "swiglu_gate", "swiglu_gate_packed",
-           "apply_rope", "fused_linear_cross_entropy", "MAX_NORM_DIM"]
+           "apply_rope", "fused_linear_cross_entropy", "topk_sample", "MAX_NORM_DIM", "MAX_SAMPLE_VOCAB"]
 
 MAX_NORM_DIM = 4096
+MAX_SAMPLE_VOCAB = 32768  # vocabulary of one topk_sample row (1024 threads x 32 values in registers)
 _DT = {torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16, torch.float32: _native.DTYPE_FP32}
 _DTYPE_OF = {v: k for k, v in _DT.items()}
 
@@ -469,6 +470,41 @@ def swiglu_bwd(gate: torch.Tensor, up: torch.Tensor, dout: torch.Tensor) -> tupl
 def _swiglu_bwd_fake(gate, up, dout):
     return (torch.empty_like(gate, memory_format=torch.contiguous_format),
             torch.empty_like(gate, memory_format=torch.contiguous_format))
+
+
+def topk_sample(logits: torch.Tensor, noise: torch.Tensor, k: int) -> torch.Tensor:
+    """One token per row of fp32 ``logits`` [rows, vocab]: keep the values >=
+    the k-th largest (ties included), p = softmax over them, return [rows, 1]
+    int64 = the first index of the largest p / ``noise`` (Exponential(1)
+    draws, same shape) -- the draw ``torch.multinomial(probs, 1)`` makes after
+    the reference's top-k mask (``model.py:141-145``), in one launch
+    (``mt_topk_sample``)."""
+    if not logits.is_cuda or logits.dtype != torch.float32 or logits.ndim != 2:
+        raise RuntimeError("topk_sample takes fp32 [rows, vocab] GPU logits")
+    if noise.shape != logits.shape or noise.dtype != torch.float32 or noise.device != logits.device:
+        raise ValueError("noise must be fp32 with the logits' shape and device")
+    if not 1 <= k <= logits.shape[1] or logits.shape[1] > MAX_SAMPLE_VOCAB:
+        raise ValueError(f"need 1 <= k <= vocab <= {MAX_SAMPLE_VOCAB} (k={k}, vocab={logits.shape[1]})")
+    return torch.ops.mega_trading_amd.topk_sample(logits, noise, k)
+
+
+@torch.library.custom_op("mega_trading_amd::topk_sample", mutates_args=(), device_types="cuda")
+def _topk_sample_op(logits: torch.Tensor, noise: torch.Tensor, k: int) -> torch.Tensor:
+    lib = _native.load()
+    x = logits if logits.stride(1) == 1 else logits.contiguous()
+    e = noise if noise.stride(1) == 1 else noise.contiguous()
+    rows, vocab = x.shape
+    out = torch.empty((rows, 1), device=x.device, dtype=torch.int64)
+    with torch.cuda.device(x.device):
+        rc = lib.mt_topk_sample(x.data_ptr(), x.stride(0), e.data_ptr(), e.stride(0), rows, vocab, k, out.data_ptr(),
+                                _native.DTYPE_FP32, _stream(x))
+    _native.check(rc, "mt_topk_sample")
+    return out
+
+
+@_topk_sample_op.register_fake
+def _topk_sample_fake(logits, noise, k):
+    return logits.new_empty((logits.shape[0], 1), dtype=torch.int64)
 
 
 @torch.library.custom_op("mega_trading_amd::swiglu_packed_fwd", mutates_args=(), device_types="cuda")

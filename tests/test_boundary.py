@@ -148,6 +148,16 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     assert lib.mt_linear_rows(p, 512, ws, (ctypes.c_int * 2)(64, 0), ld, 2, p, 96, 32, 512, FP32, None) == -2
     assert lib.mt_linear_rows(p, 512, None, ns, ld, 2, p, 96, 32, 512, FP32, None) == -1
     assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, None, 96, 32, 512, FP32, None) == -1
+    # top-k sampling: fp32, 1 <= k <= vocab <= 32768, row strides >= vocab
+    assert lib.mt_topk_sample(p, 128, p, 128, 4, 128, 16, p, BF16, None) == -4
+    assert lib.mt_topk_sample(p, 128, p, 128, 4, 0, 1, p, FP32, None) == -2
+    assert lib.mt_topk_sample(p, 40000, p, 40000, 4, 40000, 16, p, FP32, None) == -2
+    assert lib.mt_topk_sample(p, 128, p, 128, 4, 128, 129, p, FP32, None) == -2
+    assert lib.mt_topk_sample(p, 128, p, 128, 4, 128, 0, p, FP32, None) == -2
+    assert lib.mt_topk_sample(p, 127, p, 128, 4, 128, 16, p, FP32, None) == -3
+    assert lib.mt_topk_sample(p, 128, p, 100, 4, 128, 16, p, FP32, None) == -3
+    assert lib.mt_topk_sample(p, 128, None, 128, 4, 128, 16, p, FP32, None) == -1
+    assert lib.mt_topk_sample(None, 128, None, 128, 0, 128, 16, None, FP32, None) == 0  # no rows: nothing to do
 
 
 def test_ops_reject_cpu_tensors(mta):
@@ -330,6 +340,8 @@ def test_fake_impls_give_shapes_for_tracing(mta):
         y = torch.ops.mega_trading_amd.linear_rows(_fake((32, 512), torch.float32),
                                                    [_fake((768, 512), torch.float32), _fake((64, 512), torch.float32)])
         assert y.shape == (32, 832) and y.dtype == torch.float32
+        tok = torch.ops.mega_trading_amd.topk_sample(_fake((32, 16384), torch.float32), _fake((32, 16384), torch.float32), 16)
+        assert tok.shape == (32, 1) and tok.dtype == torch.int64
 
 
 def test_kernel_ready_keeps_model_layout_views():
