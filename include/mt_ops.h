@@ -175,11 +175,14 @@ int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B,
  * results side by side in y's rows (y row stride y_row_stride >= the sum of
  * out_features).  `weights` and `out_features`, `w_row_strides` are host arrays
  * (device pointers in `weights`).  x is [rows, in_features] with row stride
- * x_row_stride.  One launch reads every weight in place (no concatenation): the
- * decode step's q|k|v and w1|w3 projections.  dtype MT_DTYPE_FP32 only;
+ * x_row_stride, of type `dtype`: MT_DTYPE_FP32, or MT_DTYPE_BF16 / MT_DTYPE_FP16
+ * (widened to fp32 exactly, as x.float() would); weights and y are fp32.  One
+ * launch reads every weight in place (no concatenation): the decode step's
+ * q|k|v and w1|w3 projections, and o_proj on the 16-bit attention output.
  * 1 <= groups <= 4; 1 <= rows <= 64; in_features a positive multiple of 128;
- * x and the weights 16-byte aligned with row strides that are multiples of 4.
- * Sums in fp32 (MFMA), in an order of this kernel's own. */
+ * weights 16-byte aligned, x 16-byte (fp32) or 8-byte (16-bit) aligned, row
+ * strides multiples of 4 elements.  Sums in fp32 (MFMA), in an order of this
+ * kernel's own. */
 int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weights, const int* out_features,
                    const int64_t* w_row_strides, int groups, void* y, int64_t y_row_stride, int rows, int in_features,
                    int dtype, void* stream);

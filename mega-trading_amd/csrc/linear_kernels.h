@@ -1,7 +1,8 @@
 // gfx950 fp32 products of a few rows against grouped weights: the decode
 // step's projections.  y[m, off_g + n] = sum_k x[m, k] w_g[n, k] for every
 // group g (the q, k and v projections of a layer, or its w1 and w3), from one
-// launch that reads each weight matrix where it lies: the "hip" decoder's
+// launch that reads each weight matrix where it lies (and x as it lies, fp32
+// or 16-bit: the decode attention's output): the "hip" decoder's
 // packed GEMM otherwise concatenates the weights first (a copy of every
 // weight per call), and the library GEMMs at 32 rows are latency-bound.
 //
@@ -17,6 +18,8 @@
 // fp32 throughout (the reference's eval runs the fp32 model without
 // autocast).
 #pragma once
+
+#include <type_traits>
 
 #include "mt_common.h"
 
@@ -36,7 +39,7 @@ struct LinearGroup {
 };
 
 struct LinearParams {
-  const float* x;   // [M, K], row stride ldx
+  const void* x;    // [M, K], row stride ldx: fp32, or 16-bit (converted to fp32 on load)
   float* y;         // [M, >= sum n], row stride ldy
   int64_t ldx, ldy;
   int M, K, groups;
@@ -45,8 +48,21 @@ struct LinearParams {
 
 // MFMA layout (16x16x4, fp32): A[i][k] from lane i + 16 k, B[k][j] from lane
 // j + 16 k; lane l holds D[4 (l / 16) + v][l % 16], v = 0..3.
-// PD: 16-byte chunks per lane held in flight (all of them when K <= 128 PD).
-template <int PD>
+// 4 consecutive x values as fp32: one 16-byte load, or one 8-byte load of
+// 16-bit values (E = BF16 / FP16) widened exactly
+template <class E>
+__device__ __forceinline__ f32x4 load_x4(const void* row, int k) {
+  if constexpr (std::is_same_v<E, float>) {
+    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + k);
+  } else {
+    const u32x2 w = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(row) + k);
+    return f32x4{lo_f<E>(w[0]), hi_f<E>(w[0]), lo_f<E>(w[1]), hi_f<E>(w[1])};
+  }
+}
+
+// PD: chunks of 4 values per lane held in flight (all of them when K <= 128 PD).
+// XT: float, or BF16 / FP16 for a 16-bit x.
+template <int PD, class XT>
 __global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearParams p) {
   __shared__ float red[kLinWaves][16][17];
   const int tid = threadIdx.x;
@@ -68,17 +84,19 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearP
   const int S = p.K >> 5;
   const int k0 = (4 * wave + q) * S;
   const float* wrow = grp.w + (int64_t)min(n0 + c, grp.n - 1) * grp.ldw + k0;
-  const float* xrow = p.x + (int64_t)min(m0 + c, p.M - 1) * p.ldx + k0;
+  constexpr int XB = std::is_same_v<XT, float> ? 4 : 2;  // bytes per x value
+  const void* xrow = static_cast<const char*>(p.x) + ((int64_t)min(m0 + c, p.M - 1) * p.ldx + k0) * XB;
 
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // two chains: back-to-back issue
   const int nch = S >> 2;
   f32x4 wb[PD], xb[PD];
+  auto load = [&](int j, int kk) {
+    wb[j] = *reinterpret_cast<const f32x4*>(wrow + kk);
+    xb[j] = load_x4<XT>(xrow, kk);
+  };
 #pragma unroll
   for (int j = 0; j < PD; ++j)
-    if (j < nch) {
-      wb[j] = *reinterpret_cast<const f32x4*>(wrow + 4 * j);
-      xb[j] = *reinterpret_cast<const f32x4*>(xrow + 4 * j);
-    }
+    if (j < nch) load(j, 4 * j);
   for (int i0 = 0; i0 < nch; i0 += PD) {
 #pragma unroll
     for (int j = 0; j < PD; ++j) {
@@ -87,10 +105,7 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearP
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           acc[e & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[j][e], wb[j][e], acc[e & 1], 0, 0, 0);
-        if (i + PD < nch) {
-          wb[j] = *reinterpret_cast<const f32x4*>(wrow + 4 * (i + PD));
-          xb[j] = *reinterpret_cast<const f32x4*>(xrow + 4 * (i + PD));
-        }
+        if (i + PD < nch) load(j, 4 * (i + PD));
       }
     }
   }

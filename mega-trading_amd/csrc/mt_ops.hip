@@ -533,7 +533,8 @@ int mt_apply_rope(const void* q, const void* k, void* q_out, void* k_out, int B,
 int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weights, const int* out_features,
                    const int64_t* w_row_strides, int groups, void* y, int64_t y_row_stride, int rows, int in_features,
                    int dtype, void* stream) {
-  if (dtype != MT_DTYPE_FP32) return fail(MT_E_DTYPE, "dtype code %d unsupported (fp32 only)", dtype);
+  if (dtype != MT_DTYPE_FP32 && dtype != MT_DTYPE_BF16 && dtype != MT_DTYPE_FP16)
+    return fail(MT_E_DTYPE, "x dtype code %d unsupported", dtype);
   if (groups < 1 || groups > mt::kLinGroups)
     return fail(MT_E_SHAPE, "groups must be in [1, %d] (got %d)", mt::kLinGroups, groups);
   if (rows < 1 || rows > mt::kLinMaxRows)
@@ -542,12 +543,14 @@ int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weigh
     return fail(MT_E_SHAPE, "in_features must be a positive multiple of 128 (got %d)", in_features);
   if (!weights || !out_features || !w_row_strides) return fail(MT_E_NULL, "weights, out_features or w_row_strides is NULL");
   int rc;
-  if ((rc = check_ptr("x", x))) return rc;
+  if (!x) return fail(MT_E_NULL, "x is NULL");
+  if (reinterpret_cast<uintptr_t>(x) % (dtype == MT_DTYPE_FP32 ? 16 : 8))
+    return fail(MT_E_STRIDE, "x must be %d-byte aligned", dtype == MT_DTYPE_FP32 ? 16 : 8);
   if (!y) return fail(MT_E_NULL, "y is NULL");
   if (x_row_stride < in_features || x_row_stride % 4)
     return fail(MT_E_STRIDE, "x row stride %lld must be >= in_features and a multiple of 4", (long long)x_row_stride);
   mt::LinearParams p{};
-  p.x = static_cast<const float*>(x);
+  p.x = x;
   p.y = static_cast<float*>(y);
   p.ldx = x_row_stride;
   p.ldy = y_row_stride;
@@ -576,8 +579,13 @@ int mt_linear_rows(const void* x, int64_t x_row_stride, const void* const* weigh
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)(tiles * ((rows + 15) / 16))), block(64 * mt::kLinWaves);
   // every chunk of a lane in flight at once up to K = 1536 (12 chunks of 4 values per lane)
-  if (in_features <= 128 * 12) hipLaunchKernelGGL((mt::linear_rows_f32_kernel<12>), grid, block, 0, st, p);
-  else hipLaunchKernelGGL((mt::linear_rows_f32_kernel<4>), grid, block, 0, st, p);
+#define MT_LINEAR(XT)                                                                                        \
+  if (in_features <= 128 * 12) hipLaunchKernelGGL((mt::linear_rows_f32_kernel<12, XT>), grid, block, 0, st, p); \
+  else hipLaunchKernelGGL((mt::linear_rows_f32_kernel<4, XT>), grid, block, 0, st, p)
+  if (dtype == MT_DTYPE_FP32) { MT_LINEAR(float); }
+  else if (dtype == MT_DTYPE_BF16) { MT_LINEAR(mt::BF16); }
+  else { MT_LINEAR(mt::FP16); }
+#undef MT_LINEAR
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ok() : fail((int)e, "launch failed: %s", hipGetErrorString(e));
 }

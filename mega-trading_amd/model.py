@@ -457,7 +457,11 @@ class LlamaAttention(nn.Module):
         q_rot = _hip_decode_rope_append(query, key, value, self.rope.cos, self.rope.sin, pos, k_cache, v_cache)
         out = _hip_decode_attention(q_rot, k_cache, v_cache, pos + 1 if length is None else length,
                                     repeats=self.repeats)
-        attended = out.to(hidden.dtype).transpose(1, 2).reshape(b, 1, hidden_dim)
+        if self.attention_backend != "hip":
+            out = out.to(hidden.dtype)
+        # on "hip" o_proj takes the 16-bit output as it is (the few-row product
+        # widens it on load: the same values as casting first)
+        attended = out.transpose(1, 2).reshape(b, 1, hidden_dim)
         return self._out(attended)
 
 

@@ -114,21 +114,23 @@ class _Project(torch.autograd.Function):
 
 
 _ROWS_MAX = 64     # rows of one mt_linear_rows launch
+_X_DTYPES = {torch.float32: _native.DTYPE_FP32, torch.bfloat16: _native.DTYPE_BF16, torch.float16: _native.DTYPE_FP16}
 _ROWS_GROUPS = 4   # weights of one launch
 
 
 def _rows_path(x2: torch.Tensor, weights: Sequence[torch.Tensor], dtype: torch.dtype) -> bool:
-    """Whether ``mt_linear_rows`` takes the product: no autograd, fp32 operands
-    and compute, at most 64 rows and 4 weights, in_features a multiple of 128,
-    16-byte aligned rows with unit last strides."""
-    if dtype != torch.float32 or x2.dtype != torch.float32 or x2.device.type != "cuda":
+    """Whether ``mt_linear_rows`` takes the product: no autograd, fp32 weights
+    and compute (x fp32, or 16-bit widened exactly as the promotion to fp32
+    would), at most 64 rows and 4 weights, in_features a multiple of 128,
+    aligned rows with unit last strides."""
+    if dtype != torch.float32 or x2.dtype not in _X_DTYPES or x2.device.type != "cuda":
         return False
     if torch.is_grad_enabled() and (x2.requires_grad or any(w.requires_grad for w in weights)):
         return False
     rows, k = x2.shape
     if not 1 <= rows <= _ROWS_MAX or k % 128 or len(weights) > _ROWS_GROUPS:
         return False
-    if x2.stride(1) != 1 or x2.stride(0) % 4 or x2.data_ptr() % 16:
+    if x2.stride(1) != 1 or x2.stride(0) % 4 or x2.data_ptr() % (16 if x2.dtype == torch.float32 else 8):
         return False
     return all(w.dtype == torch.float32 and w.device == x2.device and w.stride(1) == 1 and w.stride(0) % 4 == 0
                and w.data_ptr() % 16 == 0 for w in weights)
@@ -136,8 +138,9 @@ def _rows_path(x2: torch.Tensor, weights: Sequence[torch.Tensor], dtype: torch.d
 
 @torch.library.custom_op("mega_trading_amd::linear_rows", mutates_args=(), device_types="cuda")
 def linear_rows(x: torch.Tensor, weights: list[torch.Tensor]) -> torch.Tensor:
-    """[rows, sum(out_i)] = cat([x @ w.T for w in weights], -1) for fp32 x
-    [rows <= 64, K] and weights [out_i, K] (``mt_linear_rows``)."""
+    """[rows, sum(out_i)] = cat([x.float() @ w.T for w in weights], -1), fp32,
+    for x [rows <= 64, K] (fp32 or 16-bit) and fp32 weights [out_i, K]
+    (``mt_linear_rows``)."""
     lib = _native.load()
     rows, k = x.shape
     outs = [w.shape[0] for w in weights]
@@ -148,7 +151,7 @@ def linear_rows(x: torch.Tensor, weights: list[torch.Tensor]) -> torch.Tensor:
     lds = (ctypes.c_int64 * g)(*[w.stride(0) for w in weights])
     with torch.cuda.device(x.device):
         rc = lib.mt_linear_rows(x.data_ptr(), x.stride(0), ptrs, ns, lds, g, y.data_ptr(), y.stride(0), rows, k,
-                                _native.DTYPE_FP32, torch.cuda.current_stream(x.device).cuda_stream)
+                                _X_DTYPES[x.dtype], torch.cuda.current_stream(x.device).cuda_stream)
     _native.check(rc, "mt_linear_rows")
     return y
 

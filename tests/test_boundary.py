@@ -133,7 +133,8 @@ def test_ops_c_abi_rejects_bad_arguments_before_launch(mta):
     ws = (ctypes.c_void_p * 2)(p, p)
     ns = (ctypes.c_int * 2)(64, 32)
     ld = (ctypes.c_int64 * 2)(512, 512)
-    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 32, 512, BF16, None) == -4
+    assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 32, 512, 7, None) == -4
+    assert lib.mt_linear_rows(p + 4, 512, ws, ns, ld, 2, p, 96, 32, 512, BF16, None) == -3  # 16-bit x: 8-byte aligned
     assert lib.mt_linear_rows(p, 512, ws, ns, ld, 0, p, 96, 32, 512, FP32, None) == -2
     assert lib.mt_linear_rows(p, 512, ws, ns, ld, 5, p, 96, 32, 512, FP32, None) == -2
     assert lib.mt_linear_rows(p, 512, ws, ns, ld, 2, p, 96, 65, 512, FP32, None) == -2

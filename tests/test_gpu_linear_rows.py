@@ -45,6 +45,18 @@ def test_linear_rows_against_float64(rows, k, outs):
     assert err <= 1e-5 * ref.abs().max().item() + 1e-6, err
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_linear_rows_widens_16bit_x_exactly(dt):
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(32, 512, generator=g).to(dt).cuda()
+    ws = [(torch.randn(n, 512, generator=g) / 22.6).cuda() for n in (512, 64)]
+    y = proj.linear_rows(x, ws)
+    assert (y.double() - _ref(x.float(), ws)).abs().max().item() <= 1e-5
+    with torch.no_grad():  # the promotion path of project_packed: 16-bit x, fp32 weights
+        z = proj.project_packed(x.view(32, 1, 512), ws)
+    assert torch.equal(z.view(32, -1), y)
+
+
 def test_linear_rows_reads_strided_rows_in_place():
     # x rows with a larger stride, weights that are row blocks of a wider matrix
     g = torch.Generator().manual_seed(7)
