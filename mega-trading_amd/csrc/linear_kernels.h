@@ -7,10 +7,11 @@
 // weight per call), and the library GEMMs at 32 rows are latency-bound.
 //
 // One workgroup per 16 x 16 tile of y (16 rows, 16 columns of one group),
-// 8 waves; the contraction is cut into 32 segments of K / 32 values, wave w
-// and lane quarter q taking segment 4 w + q.  A lane loads its segment of one
-// x row and one w row as 16-byte chunks, all of them before the first product
-// (up to 12 chunks: one memory round trip for K <= 1536), and feeds them to
+// 8 waves; wave w takes K / 8 values of the contraction, and its lane quarter
+// q every fourth 16-byte block of them, so that the four quarters of a row
+// read 64 contiguous bytes per load instruction.  A lane loads its blocks of
+// one x row and one w row, all of them before the first product (up to 12:
+// one memory round trip for K <= 1536), and feeds them to
 // v_mfma_f32_16x16x4_f32, whose contraction slot is the lane quarter, so the
 // four quarters' partial sums add inside the MFMA; the 8 waves' tiles are
 // summed through LDS.  Row tiles are separate workgroups so that narrow
@@ -80,15 +81,16 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearP
   const LinearGroup grp = p.g[gi];
   const int n0 = (ct - grp.tile0) * kLinCols;
 
-  // this lane's segment of the contraction: S = K / 32 values, S % 4 == 0
-  const int S = p.K >> 5;
-  const int k0 = (4 * wave + q) * S;
+  // the contraction: wave w takes the values [w K / 8, (w + 1) K / 8), and of
+  // those lane quarter q the 16-byte blocks 4 j + q (j = 0 .. K / 128 - 1), so
+  // for each j the four quarters of a row read 64 contiguous bytes
+  const int k0 = wave * (p.K >> 3) + 4 * q;
   const float* wrow = grp.w + (int64_t)min(n0 + c, grp.n - 1) * grp.ldw + k0;
   constexpr int XB = std::is_same_v<XT, float> ? 4 : 2;  // bytes per x value
   const void* xrow = static_cast<const char*>(p.x) + ((int64_t)min(m0 + c, p.M - 1) * p.ldx + k0) * XB;
 
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // two chains: back-to-back issue
-  const int nch = S >> 2;
+  const int nch = p.K >> 7;
   f32x4 wb[PD], xb[PD];
   auto load = [&](int j, int kk) {
     wb[j] = *reinterpret_cast<const f32x4*>(wrow + kk);
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearP
   };
 #pragma unroll
   for (int j = 0; j < PD; ++j)
-    if (j < nch) load(j, 4 * j);
+    if (j < nch) load(j, 16 * j);
   for (int i0 = 0; i0 < nch; i0 += PD) {
 #pragma unroll
     for (int j = 0; j < PD; ++j) {
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_rows_f32_kernel(LinearP
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           acc[e & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[j][e], wb[j][e], acc[e & 1], 0, 0, 0);
-        if (i + PD < nch) load(j, 4 * (i + PD));
+        if (i + PD < nch) load(j, 16 * (i + PD));
       }
     }
   }
