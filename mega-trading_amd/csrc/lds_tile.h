@@ -104,35 +104,47 @@ struct Tile {
 // prefetch with the current tile's compute.  Completion is enforced explicitly:
 // every copied buffer is read only after wait_vmem() and a workgroup barrier,
 // and a buffer is refilled only after the barrier that ends its last reads.
+//
+// Because the compiler does not see what these instructions read, it cannot
+// insert the wait states gfx950 requires before them, so the blocks take care
+// of them: each starts with `s_nop 0` after the M0 write the compiler places
+// right before it (an LDS DMA reading an M0 written by a scalar instruction
+// needs one wait state), and the scalar-base forms read their base from a
+// scalar copy (uniform_ptr), never from the SGPRs a v_readfirstlane wrote (a
+// vector-memory instruction reading an SGPR written by a vector instruction
+// needs five).
 __device__ __forceinline__ uint32_t lds_addr(const void* l) {
   return (uint32_t)(uintptr_t)l;
 }
 
 __device__ __forceinline__ void lds_dma16(const uint16_t* g, char* l) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
 }
 
 __device__ __forceinline__ void lds_dma4(const float* g, char* l) {
-  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_addr(l)));
 }
 
 // Scalar-base forms: lane L reads base + voff_L (a 32-bit byte offset), so a
 // whole tile's addresses cost one 64-bit scalar add and no vector ALU work.
 // `base` must be wave-uniform; it is moved to scalar registers explicitly
-// (free when the compiler already holds it there).
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+// (free when the compiler already holds it there) and then copied by a scalar
+// instruction, which the copy blocks read.
+__device__ __forceinline__ uint64_t uniform_ptr(const void* p) {
   const uint64_t v = (uint64_t)(uintptr_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  uint64_t r;
+  asm volatile("s_mov_b64 %0, %1" : "=s"(r) : "s"(((uint64_t)hi << 32) | lo));
+  return r;
 }
 
 __device__ __forceinline__ void lds_dma16_s(const void* base, uint32_t voff, uint32_t l) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(l));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(l));
 }
 
 __device__ __forceinline__ void lds_dma4_s(const void* base, uint32_t voff, uint32_t l) {
-  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(l));
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(base)), "{m0}"(l));
 }
 
 // Staging of one 64-row tile by the NW waves of a workgroup: per-lane source
